@@ -1,0 +1,73 @@
+"""Build script for the gfx950 kernel library and its C++ API layer.
+
+    python -m evk_amd.build            # builds evk_amd/libevkhip.so and evk_amd/libevk.so
+
+libevkhip.so  - the C ABI of include/evkhip.h (hipcc, --offload-arch=gfx950)
+libevk.so     - the evk / evk::ai C++ API of include/evk.h, include/evk_ai.h,
+                implemented over libevkhip.so
+Both are written in-tree so they travel with the repository snapshot.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("EVK_OFFLOAD_ARCH", "gfx950")
+
+KERNEL_SOURCES = ["capi.hip", "gemm.hip", "flash.hip", "decode_ops.hip", "model.hip"]
+API_SOURCES = ["evk_runtime.cpp", "evk_ai.cpp"]
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # packed fp32 instructions are kept out of the device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"), "-Wno-unused-result",
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("build failed:\n" + " ".join(cmd) + "\n" + r.stdout + r.stderr)
+    return r
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    cmd = [HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [HIPCC, "-x", "hip"] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    _run(cmd)
+    return obj
+
+
+def build(verbose: bool = False) -> None:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = KERNEL_SOURCES + [s for s in API_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    kern = os.path.join(HERE, "libevkhip.so")
+    tmp = kern + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [objs[s] for s in KERNEL_SOURCES])
+    os.replace(tmp, kern)
+    api = [objs[s] for s in API_SOURCES if s in objs]
+    if api:
+        lib = os.path.join(HERE, "libevk.so")
+        tmp = lib + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + api +
+             ["-L", HERE, "-levkhip", "-Wl,-rpath,$ORIGIN"])
+        os.replace(tmp, lib)
+    if verbose:
+        print("built", kern)
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

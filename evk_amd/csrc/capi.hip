@@ -1,0 +1,318 @@
+// C ABI entry points (include/evkhip.h): argument and shape validation on the
+// host, then dispatch to the gfx950 kernels.  Validation mirrors the asserts
+// of the reference wrappers (evk_ai.cpp) but reports a status code instead of
+// aborting, and relaxes the tile-divisibility rules (matmul accepts any M, N,
+// K; flash attention any N).
+#include "kernels.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+namespace evkhip {
+
+
+// ---------------------------------------------------------------------------
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    return set_error(EVKHIP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int device_cu_count() {
+    static int cached_dev = -1, cached_cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return cached_cus;
+    if (dev != cached_dev) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            cached_cus = cus;
+        cached_dev = dev;
+    }
+    return cached_cus;
+}
+
+int check_tensor(const evkhip_tensor* t, const char* name, uint32_t min_rank, uint32_t max_rank) {
+    if (!t) return set_error(EVKHIP_ERR_INVALID_ARG, "%s: null tensor descriptor", name);
+    if (t->rank < min_rank || t->rank > max_rank)
+        return set_error(EVKHIP_ERR_SHAPE, "%s: rank %u not in [%u,%u]", name, t->rank, min_rank, max_rank);
+    if (numel(t) > 0 && !t->data) return set_error(EVKHIP_ERR_INVALID_ARG, "%s: null data pointer", name);
+    return EVKHIP_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static bool same_shape(const evkhip_tensor* a, const evkhip_tensor* b) {
+    if (a->rank != b->rank) return false;
+    for (uint32_t i = 0; i < a->rank; ++i)
+        if (a->dims[i] != b->dims[i]) return false;
+    return true;
+}
+
+}  // namespace evkhip
+
+using namespace evkhip;
+
+#define CHECK(expr)                 \
+    do {                            \
+        int _rc = (expr);           \
+        if (_rc) return _rc;        \
+    } while (0)
+
+extern "C" {
+
+const char* evkhip_version(void) { return "evkhip 0.1 gfx950"; }
+
+const char* evkhip_last_error(void) { return g_err; }
+
+int evkhip_init(void) {
+    int dev = 0;
+    EVK_HIP(hipGetDevice(&dev));
+    (void)device_cu_count();
+    return EVKHIP_OK;
+}
+
+int evkhip_shutdown(void) {
+    gemm_free_workspace();
+    flash_free_workspace();
+    decode_ops_free_workspace();
+    model_free_workspace();
+    return EVKHIP_OK;
+}
+
+int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
+                  int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream) {
+    CHECK(check_tensor(a, "matmul: a", 2, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(b, "matmul: b", 2, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(c, "matmul: c", 2, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF((tile_m % 16) || (tile_n % 16), EVKHIP_ERR_INVALID_ARG,
+                  "matmul: tile hints must be multiples of 16 (got %u, %u)", tile_m, tile_n);
+    // evk_ai.cpp:261-268: batch = max, inputs may broadcast, C must match
+    const uint64_t bA = a->rank >= 3 ? batch_of(a, 2) : 1, bB = b->rank >= 3 ? batch_of(b, 2) : 1;
+    const uint64_t bC = c->rank >= 3 ? batch_of(c, 2) : 1;
+    const uint64_t batch = std::max({bA, bB, bC});
+    EVK_RETURN_IF(!(bA == batch || bA == 1) || !(bB == batch || bB == 1) || bC != batch, EVKHIP_ERR_SHAPE,
+                  "matmul: batch mismatch (a %llu, b %llu, c %llu)", (unsigned long long)bA,
+                  (unsigned long long)bB, (unsigned long long)bC);
+    // evk_ai.cpp:273-288: logical dims from the transpose flags
+    const uint32_t M = transpose_a ? dim_at(a, -1) : dim_at(a, -2);
+    const uint32_t K = transpose_a ? dim_at(a, -2) : dim_at(a, -1);
+    const uint32_t Kb = transpose_b ? dim_at(b, -1) : dim_at(b, -2);
+    const uint32_t N = transpose_b ? dim_at(b, -2) : dim_at(b, -1);
+    EVK_RETURN_IF(K != Kb, EVKHIP_ERR_SHAPE, "matmul: inner dims differ (%u vs %u)", K, Kb);
+    EVK_RETURN_IF(dim_at(c, -2) != M || dim_at(c, -1) != N, EVKHIP_ERR_SHAPE,
+                  "matmul: c is (%u,%u), expected (%u,%u)", dim_at(c, -2), dim_at(c, -1), M, N);
+    EVK_RETURN_IF(batch > 65535 || M > (1u << 30) || N > (1u << 30), EVKHIP_ERR_UNSUPPORTED,
+                  "matmul: sizes beyond the kernel's grid limits");
+    if (batch == 0 || M == 0 || N == 0) return EVKHIP_OK;
+    GemmArgs g{};
+    g.A = (const f16*)a->data;
+    g.B = (const f16*)b->data;
+    g.C = (f16*)c->data;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.sA = (bA == 1 && batch > 1) ? 0 : (int64_t)dim_at(a, -2) * dim_at(a, -1);
+    g.sB = (bB == 1 && batch > 1) ? 0 : (int64_t)dim_at(b, -2) * dim_at(b, -1);
+    g.sC = (int64_t)M * N;
+    g.acc = acc_c ? 1 : 0;
+    const bool vec_ok = aligned16(a->data) && aligned16(b->data) && aligned16(c->data) &&
+                        (dim_at(a, -1) % 8 == 0) && (dim_at(b, -1) % 8 == 0) && (N % 8 == 0) &&
+                        (K % 8 == 0) && (M % 8 == 0 || !transpose_a) && (g.sA % 8 == 0) &&
+                        (g.sB % 8 == 0);
+    if (K == 0) {
+        // C = 0 (or unchanged with acc): a GEMM with an empty contraction
+        if (acc_c) return EVKHIP_OK;
+        EVK_HIP(hipMemsetAsync(c->data, 0, numel(c) * 2, as_stream(stream)));
+        return EVKHIP_OK;
+    }
+    return gemm_dispatch(g, (int)batch, transpose_a != 0, transpose_b != 0, vec_ok, as_stream(stream));
+}
+
+static int flash_shapes(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
+                        const char* op, uint32_t* B, uint32_t* N, uint32_t* D, uint32_t* Dh) {
+    CHECK(check_tensor(q, "flash: q", 3, 3));
+    CHECK(check_tensor(k, "flash: k", 3, 3));
+    CHECK(check_tensor(v, "flash: v", 3, 3));
+    *B = q->dims[0];
+    *N = q->dims[1];
+    *D = q->dims[2];
+    *Dh = k->dims[2];
+    EVK_RETURN_IF(k->dims[0] != *B || k->dims[1] != *N, EVKHIP_ERR_SHAPE, "%s: k must be (B,N,Dh)", op);
+    EVK_RETURN_IF(!same_shape(k, v), EVKHIP_ERR_SHAPE, "%s: v must match k", op);
+    EVK_RETURN_IF(*Dh == 0 || *D % *Dh != 0, EVKHIP_ERR_SHAPE, "%s: D=%u not a multiple of Dh=%u", op, *D, *Dh);
+    EVK_RETURN_IF(*Dh > 256, EVKHIP_ERR_UNSUPPORTED, "%s: Dh=%u > 256", op, *Dh);
+    EVK_RETURN_IF((uint64_t)*N * (*D / *Dh) > (1u << 30), EVKHIP_ERR_UNSUPPORTED, "%s: N*H too large", op);
+    EVK_RETURN_IF(*B > 65535, EVKHIP_ERR_UNSUPPORTED, "%s: B too large", op);
+    return EVKHIP_OK;
+}
+
+int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
+                           const evkhip_tensor* o, int causal, float* lse, void* stream) {
+    uint32_t B, N, D, Dh;
+    CHECK(flash_shapes(q, k, v, "flash_attention", &B, &N, &D, &Dh));
+    CHECK(check_tensor(o, "flash_attention: o", 3, 3));
+    EVK_RETURN_IF(!same_shape(q, o), EVKHIP_ERR_SHAPE, "flash_attention: o must match q");
+    if (B == 0 || N == 0) return EVKHIP_OK;
+    const bool mfma = (Dh == 32 || Dh == 64 || Dh == 128) && aligned16(q->data) && aligned16(k->data) &&
+                      aligned16(v->data) && aligned16(o->data);
+    FlashArgs a{};
+    a.q = (const f16*)q->data;
+    a.k = (const f16*)k->data;
+    a.v = (const f16*)v->data;
+    a.out = (f16*)o->data;
+    a.lse = lse;
+    a.B = (int)B;
+    a.H = (int)(D / Dh);
+    a.N = (int)N;
+    return flash_forward(a, (int)Dh, mfma, causal != 0, as_stream(stream));
+}
+
+int evkhip_flash_attention_bwd(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
+                               const evkhip_tensor* o, const evkhip_tensor* dO, const evkhip_tensor* dQ,
+                               const evkhip_tensor* dK, const evkhip_tensor* dV, uint32_t heads, int causal,
+                               const float* lse, void* stream) {
+    uint32_t B, N, D, Dh;
+    CHECK(flash_shapes(q, k, v, "flash_attention_bwd", &B, &N, &D, &Dh));
+    CHECK(check_tensor(dO, "flash_attention_bwd: dO", 3, 3));
+    CHECK(check_tensor(dQ, "flash_attention_bwd: dQ", 3, 3));
+    CHECK(check_tensor(dK, "flash_attention_bwd: dK", 3, 3));
+    CHECK(check_tensor(dV, "flash_attention_bwd: dV", 3, 3));
+    EVK_RETURN_IF(!same_shape(q, dO) || !same_shape(q, dQ), EVKHIP_ERR_SHAPE,
+                  "flash_attention_bwd: dO and dQ must match q");
+    EVK_RETURN_IF(!same_shape(k, dK) || !same_shape(k, dV), EVKHIP_ERR_SHAPE,
+                  "flash_attention_bwd: dK and dV must match k");
+    const uint32_t H = D / Dh;
+    EVK_RETURN_IF(heads != 0 && heads != H, EVKHIP_ERR_SHAPE, "flash_attention_bwd: heads=%u but D/Dh=%u", heads,
+                  H);
+    if (lse) {
+        CHECK(check_tensor(o, "flash_attention_bwd: o", 3, 3));
+        EVK_RETURN_IF(!same_shape(q, o), EVKHIP_ERR_SHAPE, "flash_attention_bwd: o must match q");
+    }
+    if (B == 0 || N == 0) return EVKHIP_OK;
+    bool mfma = (Dh == 32 || Dh == 64 || Dh == 128);
+    for (const evkhip_tensor* t : {q, k, v, dO, dQ, dK, dV}) mfma = mfma && aligned16(t->data);
+    if (lse) mfma = mfma && aligned16(o->data);
+    FlashArgs a{};
+    a.q = (const f16*)q->data;
+    a.k = (const f16*)k->data;
+    a.v = (const f16*)v->data;
+    a.o = lse ? (const f16*)o->data : nullptr;
+    a.dO = (const f16*)dO->data;
+    a.out = (f16*)dQ->data;
+    a.dK = (f16*)dK->data;
+    a.dV = (f16*)dV->data;
+    a.lse = const_cast<float*>(lse);
+    a.B = (int)B;
+    a.H = (int)H;
+    a.N = (int)N;
+    return flash_backward(a, (int)Dh, mfma, causal != 0, as_stream(stream));
+}
+
+int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k_cache,
+                                  const evkhip_tensor* v_cache, const evkhip_tensor* out, uint32_t current_length,
+                                  uint32_t heads, void* stream) {
+    CHECK(check_tensor(q, "single_query_attention: q", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(k_cache, "single_query_attention: k_cache", 2, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(v_cache, "single_query_attention: v_cache", 2, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "single_query_attention: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(heads == 0, EVKHIP_ERR_INVALID_ARG, "single_query_attention: heads must be >= 1");
+    const uint64_t D = numel(q);
+    EVK_RETURN_IF(D == 0 || D % heads, EVKHIP_ERR_SHAPE, "single_query_attention: q size %llu not divisible by %u heads",
+                  (unsigned long long)D, heads);
+    EVK_RETURN_IF(numel(out) != D, EVKHIP_ERR_SHAPE, "single_query_attention: out must have q's size");
+    EVK_RETURN_IF(!same_shape(k_cache, v_cache), EVKHIP_ERR_SHAPE, "single_query_attention: caches differ");
+    EVK_RETURN_IF(dim_at(k_cache, -1) != D, EVKHIP_ERR_SHAPE,
+                  "single_query_attention: cache rows hold %u values, q has %llu", dim_at(k_cache, -1),
+                  (unsigned long long)D);
+    const uint64_t rows = numel(k_cache) / D;
+    EVK_RETURN_IF(current_length > rows, EVKHIP_ERR_SHAPE,
+                  "single_query_attention: current_length %u exceeds the %llu cached rows", current_length,
+                  (unsigned long long)rows);
+    const uint32_t dh = (uint32_t)(D / heads);
+    const bool al = aligned16(q->data) && aligned16(k_cache->data) && aligned16(v_cache->data);
+    return sq_attention_launch((const f16*)q->data, (const f16*)k_cache->data, (const f16*)v_cache->data,
+                               (f16*)out->data, (int64_t)D, (int)heads, (int)dh, (int)current_length, al,
+                               as_stream(stream));
+}
+
+int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream) {
+    CHECK(check_tensor(in, "rms_norm: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "rms_norm: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(in, out), EVKHIP_ERR_SHAPE, "rms_norm: shapes differ");
+    const uint32_t D = dim_at(in, -1);
+    if (D == 0) return EVKHIP_OK;
+    return rms_norm_launch((const f16*)in->data, (f16*)out->data, (int64_t)(numel(in) / D), (int)D, eps,
+                           as_stream(stream));
+}
+
+int evkhip_rope(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t batch_size, uint32_t seq_len,
+                uint32_t embed_dim, float rotary_base, uint32_t position_offset, uint32_t head_dim, void* stream) {
+    CHECK(check_tensor(in, "rope: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "rope: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(embed_dim % 2, EVKHIP_ERR_SHAPE, "rope: embed_dim %u must be even", embed_dim);
+    const uint32_t hd = head_dim ? head_dim : embed_dim;
+    EVK_RETURN_IF(hd == 0 || hd % 2 || embed_dim % hd, EVKHIP_ERR_SHAPE,
+                  "rope: head_dim %u must be even and divide embed_dim %u", hd, embed_dim);
+    const uint64_t n = (uint64_t)batch_size * seq_len * embed_dim;
+    EVK_RETURN_IF(numel(in) < n || numel(out) < n, EVKHIP_ERR_SHAPE, "rope: tensors hold fewer than B*S*D values");
+    return rope_launch((const f16*)in->data, (f16*)out->data, (int)batch_size, (int)seq_len, (int)embed_dim,
+                       rotary_base, (int)position_offset, (int)hd, as_stream(stream));
+}
+
+int evkhip_gelu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream) {
+    CHECK(check_tensor(in, "gelu: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "gelu: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(in, out), EVKHIP_ERR_SHAPE, "gelu: shapes differ");
+    return gelu_launch((const f16*)in->data, (f16*)out->data, (int64_t)numel(in), as_stream(stream));
+}
+
+int evkhip_add(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, void* stream) {
+    CHECK(check_tensor(a, "add: a", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(b, "add: b", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(c, "add: c", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(a, b) || !same_shape(a, c), EVKHIP_ERR_SHAPE, "add: shapes differ");
+    return add_launch((const f16*)a->data, (const f16*)b->data, (f16*)c->data, (int64_t)numel(a),
+                      as_stream(stream));
+}
+
+int evkhip_embed(const evkhip_tensor* embeddings, const evkhip_tensor* indices, const evkhip_tensor* out,
+                 void* stream) {
+    CHECK(check_tensor(embeddings, "embed: embeddings", 2, 2));
+    CHECK(check_tensor(indices, "embed: indices", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "embed: out", 1, EVKHIP_MAX_DIMS));
+    const uint32_t vocab = embeddings->dims[0], dim = embeddings->dims[1];
+    const uint64_t n_idx = numel(indices);
+    EVK_RETURN_IF(numel(out) != n_idx * dim, EVKHIP_ERR_SHAPE, "embed: out must hold indices*embed_dim values");
+    EVK_RETURN_IF(vocab == 0 && n_idx > 0, EVKHIP_ERR_SHAPE, "embed: empty table");
+    return embed_launch((const f16*)embeddings->data, (const uint16_t*)indices->data, (f16*)out->data,
+                        (int64_t)n_idx, (int)dim, (int)vocab, as_stream(stream));
+}
+
+int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out_tokens, uint32_t position,
+                         uint16_t token_base, uint16_t token_count, void* stream) {
+    CHECK(check_tensor(logits, "greedy_sample: logits", 3, 3));
+    CHECK(check_tensor(out_tokens, "greedy_sample: out_tokens", 1, 1));
+    const uint32_t B = logits->dims[0], S = logits->dims[1], V = logits->dims[2];
+    EVK_RETURN_IF(out_tokens->dims[0] != B, EVKHIP_ERR_SHAPE, "greedy_sample: out_tokens must be (B)");
+    EVK_RETURN_IF(position >= S, EVKHIP_ERR_SHAPE, "greedy_sample: position %u >= seq_len %u", position, S);
+    EVK_RETURN_IF((uint32_t)token_base + token_count > V, EVKHIP_ERR_SHAPE,
+                  "greedy_sample: token range exceeds vocab");
+    return greedy_launch((const f16*)logits->data, (uint16_t*)out_tokens->data, (int)B, (int)S, (int)V,
+                         (int)position, token_base, token_count, as_stream(stream));
+}
+
+}  // extern "C"

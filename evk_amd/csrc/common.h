@@ -1,0 +1,120 @@
+// Shared definitions for the gfx950 kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/evkhip.h"
+
+typedef _Float16 f16;
+typedef f16 half8 __attribute__((ext_vector_type(8)));
+typedef f16 half4 __attribute__((ext_vector_type(4)));
+typedef f16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------
+// Error reporting (host)
+// ---------------------------------------------------------------------------
+namespace evkhip {
+int set_error(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+hipStream_t as_stream(void* s);
+int device_cu_count();
+}  // namespace evkhip
+
+#define EVK_RETURN_IF(cond, code, ...)                  \
+    do {                                                \
+        if (cond) return evkhip::set_error(code, __VA_ARGS__); \
+    } while (0)
+
+#define EVK_HIP(expr)                                                   \
+    do {                                                                \
+        hipError_t _e = (expr);                                         \
+        if (_e != hipSuccess) return evkhip::check_hip(_e, #expr);      \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+// v_mfma_f32_32x32x16_f16: D(32x32) = A(32x16) B(16x32) + C, wave64.
+// Operand lane l holds 8 halves of row (A) / column (B) l%32 for k-group
+// l/32; the k mapping is the same for A and B, so callers only rely on:
+//   A: row = l%32, B: col = l%32, both with the same (l/32, slot) -> k.
+//   D: element j of lane l is row 8*(j/4) + 4*(l/32) + (j%4), col l%32.
+DEV floatx16 mfma32(const half8& a, const half8& b, const floatx16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+DEV uint32_t pack_h2(float lo, float hi) {
+    half2_t v = {(f16)lo, (f16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+DEV half8 as_half8(const u32x4& v) { return __builtin_bit_cast(half8, v); }
+DEV u32x4 as_u32x4(const half8& v) { return __builtin_bit_cast(u32x4, v); }
+
+// Byte permute: result bytes chosen from {hi:lo} (v_perm_b32).
+DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// (lo half of x) | (lo half of y) << 16
+DEV uint32_t pack_lo(uint32_t x, uint32_t y) { return perm_b32(y, x, 0x05040100u); }
+// (hi half of x) | (hi half of y) << 16
+DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return perm_b32(y, x, 0x07060302u); }
+
+// Transpose an 8x8 block of halves held as 8 rows of 16 bytes.
+// in[r] holds elements (r, 0..7); out[c] receives elements (0..7, c).
+DEV void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+    for (int c2 = 0; c2 < 4; ++c2) {  // column pair (2*c2, 2*c2+1) lives in dword c2
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int r2 = 0; r2 < 4; ++r2) {
+            uint32_t x = in[2 * r2][c2], y = in[2 * r2 + 1][c2];
+            lo[r2] = pack_lo(x, y);  // column 2*c2, rows 2r2, 2r2+1
+            hi[r2] = pack_hi(x, y);  // column 2*c2+1
+        }
+        out[2 * c2] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        out[2 * c2 + 1] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    }
+}
+
+DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(f16, h); }
+DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
+
+// ---------------------------------------------------------------------------
+// Host-side tensor helpers
+// ---------------------------------------------------------------------------
+namespace evkhip {
+inline uint64_t numel(const evkhip_tensor* t) {
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < t->rank; ++i) n *= t->dims[i];
+    return n;
+}
+inline uint32_t dim_at(const evkhip_tensor* t, int i) {  // negative = from the end
+    return t->dims[i < 0 ? (int)t->rank + i : i];
+}
+inline uint64_t batch_of(const evkhip_tensor* t, uint32_t inner) {  // Shape::batch_size
+    uint64_t b = 1;
+    for (uint32_t i = 0; i + inner < t->rank; ++i) b *= t->dims[i];
+    return b;
+}
+int check_tensor(const evkhip_tensor* t, const char* name, uint32_t min_rank, uint32_t max_rank);
+bool aligned16(const void* p);
+}  // namespace evkhip

@@ -1,0 +1,792 @@
+// Flash attention forward/backward for gfx950: the kernels behind
+// evk::ai::flash_attention / flash_attention_bwd (reference: evk_ai.cpp:332-473,
+// shaders/flash_attention.comp, shaders/flash_attention_bwd.comp).
+//
+// Layout (reference MQA): Q,O,dO,dQ (B,N,H*Dh); K,V,dK,dV (B,N,Dh).  Per batch
+// the query side is an (N*H) x Dh row-major matrix whose row r is query
+// position r/H of head r%H, so all heads of a position share one K/V row and
+// one K/V tile in LDS serves 8x more rows than multi-head attention would.
+//
+// MFMA mapping (v_mfma_f32_32x32x16_f16, see common.h):
+//  forward / dQ : S^T = K Q^T (keys x queries).  The D layout gives every lane
+//                 one query column and 16 keys, so the row max/sum is mostly
+//                 lane-local, and the probabilities are already the B operand
+//                 of O^T = V^T P^T.  K rows are fed to the MFMA in the order
+//                 pi(m) (bits 2 and 3 of m swapped) so that element e of a lane
+//                 holds key 16*(e/8) + 8*(l/32) + e%8: each 8-element half of
+//                 the accumulator is 8 consecutive keys, i.e. one 16-byte LDS
+//                 read of the transposed V (or K) tile.
+//  dK/dV        : S = Q K^T (queries x keys) with Q rows in the order pi, so a
+//                 lane owns one key column; dV^T += dO^T P and dK^T += Q^T dS
+//                 read dO^T / Q^T from a per-wave transposed LDS tile.
+// Softmax runs in the exp2 domain: s2 = s * scale * log2(e).
+#include "kernels.h"
+
+#include <math.h>
+
+namespace evkhip {
+
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int BC = 64;   // keys per LDS stage
+constexpr int BR = 128;  // query rows per workgroup (4 waves x 32)
+
+// pi(m): swap bits 2 and 3 of a row index in 0..31.
+DEV int pi32(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// Offset (halves) of 16-byte chunk c of row r in a tile of rows of W halves.
+template <int W>
+DEV int sw_off(int r, int c) {
+    constexpr int KC = W / 8;
+    return r * W + ((c ^ (r & (KC - 1))) << 3);
+}
+
+// Copy ROWS x DH (row-major, 16-byte chunks) from global rows [g0, g0+ROWS)
+// into registers; rows >= nrows read as zero.
+template <int ROWS, int DH, int NT>
+struct RowTile {
+    static constexpr int KC = DH / 8, CH = ROWS * KC, PER = (CH + NT - 1) / NT;
+    u32x4 r[PER];
+    DEV void load(const f16* src, int g0, int nrows) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int c = threadIdx.x + i * NT;
+            int row = c / KC, kc = c % KC;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if ((CH % NT == 0 || c < CH) && g0 + row < nrows)
+                v = *reinterpret_cast<const u32x4*>(src + (int64_t)(g0 + row) * DH + kc * 8);
+            r[i] = v;
+        }
+    }
+    DEV void store(f16* lds) const {  // [ROWS][DH] swizzled
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int c = threadIdx.x + i * NT;
+            if (CH % NT == 0 || c < CH) {
+                int row = c / KC, kc = c % KC;
+                *reinterpret_cast<u32x4*>(lds + sw_off<DH>(row, kc)) = r[i];
+            }
+        }
+    }
+};
+
+// Same rows, stored transposed in LDS as [DH][ROWS] (8x8 register transposes).
+template <int ROWS, int DH, int NT>
+struct TransTile {
+    static constexpr int RB = ROWS / 8, DB = DH / 8, BLK = RB * DB, PER = (BLK + NT - 1) / NT;
+    u32x4 r[PER][8];
+    DEV void load(const f16* src, int g0, int nrows) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + i * NT;
+            int db = q % DB, rb = q / DB;
+            bool ok = (BLK % NT == 0 || q < BLK);
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                int g = g0 + rb * 8 + rr;
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (ok && g < nrows) v = *reinterpret_cast<const u32x4*>(src + (int64_t)g * DH + db * 8);
+                r[i][rr] = v;
+            }
+        }
+    }
+    DEV void store(f16* lds) const {  // [DH][ROWS] swizzled
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int q = threadIdx.x + i * NT;
+            if (BLK % NT == 0 || q < BLK) {
+                int db = q % DB, rb = q / DB;
+                u32x4 t[8];
+                transpose8x8(r[i], t);
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    *reinterpret_cast<u32x4*>(lds + sw_off<ROWS>(db * 8 + c, rb)) = t[c];
+            }
+        }
+    }
+};
+
+DEV half8 pack8(const float* x) {
+    u32x4 u = {pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
+    return as_half8(u);
+}
+// elements [off, off+8) of an accumulator
+DEV half8 pack8v(const floatx16& x, int off) {
+    u32x4 u = {pack_h2(x[off + 0], x[off + 1]), pack_h2(x[off + 2], x[off + 3]),
+               pack_h2(x[off + 4], x[off + 5]), pack_h2(x[off + 6], x[off + 7])};
+    return as_half8(u);
+}
+
+// ---------------------------------------------------------------------------
+// Forward (MODE 0: O and public LSE) / statistics for the backward (MODE 1:
+// lse2_rows and d_rows, with dP^T = V dO^T in place of the PV product).
+// Grid: (ceil(N*H/128), B); 256 threads.
+// ---------------------------------------------------------------------------
+template <int DH, bool CAUSAL, int MODE>
+__global__ __launch_bounds__(256) void flash_fwd(FlashArgs p) {
+    constexpr int KS = DH / 16;  // k-steps of the QK^T contraction
+    constexpr int DT = DH / 32;  // 32-row dh tiles of O^T
+    __shared__ __attribute__((aligned(16))) f16 sK[2][BC * DH];
+    __shared__ __attribute__((aligned(16))) f16 sV[2][BC * DH];  // MODE 0: V^T [DH][BC]; MODE 1: V [BC][DH]
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, lg = lane >> 5;
+    const int R0 = blockIdx.x * BR;
+    const int rw0 = R0 + wave * 32;                // first row of this wave
+    const int myrow = rw0 + l32;                   // the query row of this lane
+    const bool row_ok = myrow < NH;
+    const int qpos = min(myrow, NH - 1) / H;
+    const int wpmax = min(rw0 + 31, NH - 1) / H;   // largest position in the wave
+    const int wpmin = min(rw0, NH - 1) / H;
+    const int bpmax = min(R0 + BR - 1, NH - 1) / H;
+    const int kend = CAUSAL ? min(N, bpmax + 1) : N;
+
+    const f16* Qb = p.q + (int64_t)b * NH * DH;
+    const f16* Kb = p.k + (int64_t)b * N * DH;
+    const f16* Vb = p.v + (int64_t)b * N * DH;
+
+    // Q^T fragments (B operand): lane holds row myrow, dh [16ks + 8lg, +8).
+    half8 qf[KS];
+    half8 dof[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row_ok) v = *reinterpret_cast<const u32x4*>(Qb + (int64_t)myrow * DH + ks * 16 + lg * 8);
+        qf[ks] = as_half8(v);
+        if constexpr (MODE == 1) {
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (row_ok)
+                w = *reinterpret_cast<const u32x4*>(p.dO + (int64_t)b * NH * DH + (int64_t)myrow * DH +
+                                                    ks * 16 + lg * 8);
+            dof[ks] = as_half8(w);
+        }
+    }
+
+    floatx16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[t][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, t_run = 0.0f;
+
+    RowTile<BC, DH, 256> lk;
+    RowTile<BC, DH, 256> lv_rows;    // MODE 1
+    TransTile<BC, DH, 256> lv_t;     // MODE 0
+
+    const int nkt = (kend + BC - 1) / BC;
+    if (nkt > 0) {
+        lk.load(Kb, 0, N);
+        if constexpr (MODE == 0) lv_t.load(Vb, 0, N); else lv_rows.load(Vb, 0, N);
+        lk.store(sK[0]);
+        if constexpr (MODE == 0) lv_t.store(sV[0]); else lv_rows.store(sV[0]);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nkt;
+        if (more) {
+            lk.load(Kb, (kt + 1) * BC, N);
+            if constexpr (MODE == 0) lv_t.load(Vb, (kt + 1) * BC, N); else lv_rows.load(Vb, (kt + 1) * BC, N);
+        }
+        const f16* ks_ = sK[cur];
+        const f16* vs_ = sV[cur];
+#pragma unroll
+        for (int sub = 0; sub < BC / 32; ++sub) {
+            const int key0 = kt * BC + sub * 32;
+            if (key0 < kend && (!CAUSAL || key0 <= wpmax)) {
+                floatx16 s;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+                const int arow = sub * 32 + pi32(l32);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    half8 a = *reinterpret_cast<const half8*>(ks_ + sw_off<DH>(arow, ks * 2 + lg));
+                    s = mfma32(a, qf[ks], s);
+                }
+                floatx16 dp;
+                if constexpr (MODE == 1) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) dp[e] = 0.0f;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        half8 a = *reinterpret_cast<const half8*>(vs_ + sw_off<DH>(arow, ks * 2 + lg));
+                        dp = mfma32(a, dof[ks], dp);
+                    }
+                }
+                // element e holds key key0 + 16*(e/8) + 8*lg + e%8
+                const bool need_mask = (key0 + 32 > N) || (CAUSAL && key0 + 31 > wpmin);
+                float mloc = -INFINITY;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float v = s[e] * p.scale_log2;
+                    if (need_mask) {
+                        int key = key0 + 16 * (e >> 3) + 8 * lg + (e & 7);
+                        if (key >= N || (CAUSAL && key > qpos)) v = -INFINITY;
+                    }
+                    s[e] = v;
+                    mloc = fmaxf(mloc, v);
+                }
+                mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+                const float m_new = fmaxf(m_run, mloc);
+                const float base = (m_new == -INFINITY) ? 0.0f : m_new;
+                const float alpha = exp2f(m_run - base);
+                float psum = 0.0f, tsum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float pe = exp2f(s[e] - base);
+                    s[e] = pe;
+                    psum += pe;
+                    if constexpr (MODE == 1) tsum += pe * dp[e];
+                }
+                l_run = l_run * alpha + psum;
+                m_run = m_new;
+                if constexpr (MODE == 1) {
+                    t_run = t_run * alpha + tsum;
+                } else {
+                    half8 pb0 = pack8v(s, 0);
+                    half8 pb1 = pack8v(s, 8);
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
+                        const int vrow = t * 32 + l32;  // dh
+                        half8 a0 = *reinterpret_cast<const half8*>(vs_ + sw_off<BC>(vrow, sub * 4 + 0 + lg));
+                        half8 a1 = *reinterpret_cast<const half8*>(vs_ + sw_off<BC>(vrow, sub * 4 + 2 + lg));
+                        oacc[t] = mfma32(a0, pb0, oacc[t]);
+                        oacc[t] = mfma32(a1, pb1, oacc[t]);
+                    }
+                }
+            }
+        }
+        if (more) {
+            lk.store(sK[cur ^ 1]);
+            if constexpr (MODE == 0) lv_t.store(sV[cur ^ 1]); else lv_rows.store(sV[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+
+    // both halves of the wave hold partial sums for the same query: combine
+    // them with every lane active
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float t_tot = t_run + __shfl_xor(t_run, 32, 64);
+    const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (!row_ok) return;
+    const int h = myrow % H;
+    if constexpr (MODE == 0) {
+        f16* Ob = p.out + (int64_t)b * NH * DH + (int64_t)myrow * DH;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int dh = t * 32 + 8 * e4 + 4 * lg;
+                u32x2 w = {pack_h2(oacc[t][4 * e4] * inv_l, oacc[t][4 * e4 + 1] * inv_l),
+                           pack_h2(oacc[t][4 * e4 + 2] * inv_l, oacc[t][4 * e4 + 3] * inv_l)};
+                *reinterpret_cast<u32x2*>(Ob + dh) = w;
+            }
+        if (p.lse && lg == 0) {
+            float lse = (l_tot > 0.0f) ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+            p.lse[((int64_t)b * H + h) * N + qpos] = lse;
+        }
+    } else {
+        if (lg == 0) {
+            p.lse2_rows[(int64_t)b * NH + myrow] = (l_tot > 0.0f) ? m_run + log2f(l_tot) : INFINITY;
+            p.d_rows[(int64_t)b * NH + myrow] = t_tot * inv_l;
+        }
+    }
+}
+
+// lse2_rows / d_rows from a saved LSE and O: D_i = rowsum(dO_i * O_i).
+template <int DH>
+__global__ __launch_bounds__(256) void flash_bwd_pre(FlashArgs p) {
+    const int NH = p.N * p.H;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)p.B * NH) return;
+    const int b = (int)(idx / NH), r = (int)(idx % NH);
+    const f16* o = p.o + idx * DH;
+    const f16* g = p.dO + idx * DH;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DH / 8; ++c) {
+        half8 x = *reinterpret_cast<const half8*>(o + c * 8);
+        half8 y = *reinterpret_cast<const half8*>(g + c * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
+    }
+    p.d_rows[idx] = acc;
+    const float l = p.lse[((int64_t)b * p.H + (r % p.H)) * p.N + r / p.H];
+    p.lse2_rows[idx] = l * kLog2e;
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV.  Grid: (ceil(N/32), B); 4 waves share a 32-key block whose K and V
+// fragments stay in registers; the waves take 32-row query tiles round-robin
+// and meet in LDS at the end.
+// ---------------------------------------------------------------------------
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_bwd_dkdv(FlashArgs p) {
+    constexpr int KS = DH / 16, DT = DH / 32;
+    // per wave: Q^T and dO^T tiles [DH][32]; reused as the fp32 reduction area
+    constexpr int WAVE_HALVES = 2 * DH * 32;
+    __shared__ __attribute__((aligned(16))) f16 smem[4 * WAVE_HALVES];
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, lg = lane >> 5;
+    const int key0 = blockIdx.x * 32;
+    const int mykey = key0 + l32;
+    const bool key_ok = mykey < N;
+
+    const f16* Qb = p.q + (int64_t)b * NH * DH;
+    const f16* dOb = p.dO + (int64_t)b * NH * DH;
+    const float* lse2 = p.lse2_rows + (int64_t)b * NH;
+    const float* Dr = p.d_rows + (int64_t)b * NH;
+
+    // K^T and V^T as B operands: lane holds key mykey, dh [16ks + 8lg, +8).
+    half8 kf[KS], vf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
+        if (key_ok) {
+            a = *reinterpret_cast<const u32x4*>(p.k + ((int64_t)b * N + mykey) * DH + ks * 16 + lg * 8);
+            c = *reinterpret_cast<const u32x4*>(p.v + ((int64_t)b * N + mykey) * DH + ks * 16 + lg * 8);
+        }
+        kf[ks] = as_half8(a);
+        vf[ks] = as_half8(c);
+    }
+
+    floatx16 dk[DT], dv[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { dk[t][e] = 0.0f; dv[t][e] = 0.0f; }
+
+    f16* sQt = smem + wave * WAVE_HALVES;  // [DH][32]
+    f16* sDt = sQt + DH * 32;              // [DH][32]
+
+    const int rstart = CAUSAL ? (key0 * H) / 32 * 32 : 0;
+    const int ntile = (NH - rstart + 31) / 32;
+    for (int ti = wave; ti < ntile; ti += 4) {
+        const int q0 = rstart + ti * 32;
+        // this lane's A-operand row: query q0 + pi(l32)
+        const int arow = q0 + pi32(l32);
+        const bool arow_ok = arow < NH;
+        floatx16 s, dp;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { s[e] = 0.0f; dp[e] = 0.0f; }
+        // Stage Q^T, dO^T for this tile: lane writes its row's 8 dh values.
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u32x4 qa = {0u, 0u, 0u, 0u}, ga = {0u, 0u, 0u, 0u};
+            if (arow_ok) {
+                qa = *reinterpret_cast<const u32x4*>(Qb + (int64_t)arow * DH + ks * 16 + lg * 8);
+                ga = *reinterpret_cast<const u32x4*>(dOb + (int64_t)arow * DH + ks * 16 + lg * 8);
+            }
+            half8 qh = as_half8(qa), gh = as_half8(ga);
+            s = mfma32(qh, kf[ks], s);
+            dp = mfma32(gh, vf[ks], dp);
+            // transposed store: column index = query offset pi(l32) within the tile
+            const int qc = pi32(l32);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int dh = ks * 16 + lg * 8 + e;
+                sQt[dh * 32 + qc] = qh[e];
+                sDt[dh * 32 + qc] = gh[e];
+            }
+        }
+        // element e: query q0 + 16*(e/8) + 8*lg + e%8, key mykey
+        float pe[16], dse[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int qr = q0 + 16 * (e >> 3) + 8 * lg + (e & 7);
+            float pv = 0.0f, dsv = 0.0f;
+            if (qr < NH && key_ok && (!CAUSAL || mykey <= qr / H)) {
+                pv = exp2f(s[e] * p.scale_log2 - lse2[qr]);
+                dsv = pv * (dp[e] - Dr[qr]);
+            }
+            pe[e] = pv;
+            dse[e] = dsv;
+        }
+        const half8 pb0 = pack8(&pe[0]), pb1 = pack8(&pe[8]);
+        const half8 sb0 = pack8(&dse[0]), sb1 = pack8(&dse[8]);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS stores of this wave done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int dh = t * 32 + l32;
+            // A operand rows dh, slots = queries 16*kstep + 8*lg + (0..7)
+            half8 g0 = *reinterpret_cast<const half8*>(sDt + dh * 32 + 0 + lg * 8);
+            half8 g1 = *reinterpret_cast<const half8*>(sDt + dh * 32 + 16 + lg * 8);
+            half8 q0h = *reinterpret_cast<const half8*>(sQt + dh * 32 + 0 + lg * 8);
+            half8 q1h = *reinterpret_cast<const half8*>(sQt + dh * 32 + 16 + lg * 8);
+            dv[t] = mfma32(g0, pb0, dv[t]);
+            dv[t] = mfma32(g1, pb1, dv[t]);
+            dk[t] = mfma32(q0h, sb0, dk[t]);
+            dk[t] = mfma32(q1h, sb1, dk[t]);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // Reduce the 4 waves: fp32 [wave][DT][16][64] for dk then dv.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+    constexpr int PERW = DT * 16 * 64;  // floats per wave per tensor
+    static_assert(4 * PERW * 4 <= (int)sizeof(smem), "reduction area");
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                red[wave * PERW + (t * 16 + e) * 64 + lane] = pass == 0 ? dk[t][e] : dv[t][e];
+        __syncthreads();
+        if (wave == 0) {
+            f16* dst = (pass == 0 ? p.dK : p.dV) + ((int64_t)b * N) * DH;
+            const float sc = pass == 0 ? p.scale : 1.0f;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int i = (t * 16 + e) * 64 + lane;
+                    float v = red[i] + red[PERW + i] + red[2 * PERW + i] + red[3 * PERW + i];
+                    const int dh = t * 32 + 8 * (e >> 2) + 4 * lg + (e & 3);
+                    if (key_ok) dst[(int64_t)mykey * DH + dh] = (f16)(v * sc);
+                }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ.  Grid: (ceil(N*H/128), B), like the forward.
+// ---------------------------------------------------------------------------
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_bwd_dq(FlashArgs p) {
+    constexpr int KS = DH / 16, DT = DH / 32;
+    __shared__ __attribute__((aligned(16))) f16 sK[2][BC * DH];   // K rows
+    __shared__ __attribute__((aligned(16))) f16 sV[2][BC * DH];   // V rows
+    __shared__ __attribute__((aligned(16))) f16 sKt[2][BC * DH];  // K^T [DH][BC]
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, lg = lane >> 5;
+    const int R0 = blockIdx.x * BR;
+    const int rw0 = R0 + wave * 32;
+    const int myrow = rw0 + l32;
+    const bool row_ok = myrow < NH;
+    const int qpos = min(myrow, NH - 1) / H;
+    const int wpmax = min(rw0 + 31, NH - 1) / H;
+    const int wpmin = min(rw0, NH - 1) / H;
+    const int bpmax = min(R0 + BR - 1, NH - 1) / H;
+    const int kend = CAUSAL ? min(N, bpmax + 1) : N;
+
+    const f16* Qb = p.q + (int64_t)b * NH * DH;
+    const f16* dOb = p.dO + (int64_t)b * NH * DH;
+    const f16* Kb = p.k + (int64_t)b * N * DH;
+    const f16* Vb = p.v + (int64_t)b * N * DH;
+    const float my_lse2 = row_ok ? p.lse2_rows[(int64_t)b * NH + myrow] : 0.0f;
+    const float my_d = row_ok ? p.d_rows[(int64_t)b * NH + myrow] : 0.0f;
+
+    half8 qf[KS], gf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
+        if (row_ok) {
+            a = *reinterpret_cast<const u32x4*>(Qb + (int64_t)myrow * DH + ks * 16 + lg * 8);
+            c = *reinterpret_cast<const u32x4*>(dOb + (int64_t)myrow * DH + ks * 16 + lg * 8);
+        }
+        qf[ks] = as_half8(a);
+        gf[ks] = as_half8(c);
+    }
+    floatx16 dq[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dq[t][e] = 0.0f;
+
+    RowTile<BC, DH, 256> lk, lv;
+    TransTile<BC, DH, 256> lkt;
+    const int nkt = (kend + BC - 1) / BC;
+    if (nkt > 0) {
+        lk.load(Kb, 0, N); lv.load(Vb, 0, N); lkt.load(Kb, 0, N);
+        lk.store(sK[0]); lv.store(sV[0]); lkt.store(sKt[0]);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nkt;
+        if (more) {
+            lk.load(Kb, (kt + 1) * BC, N);
+            lv.load(Vb, (kt + 1) * BC, N);
+            lkt.load(Kb, (kt + 1) * BC, N);
+        }
+#pragma unroll
+        for (int sub = 0; sub < BC / 32; ++sub) {
+            const int key0 = kt * BC + sub * 32;
+            if (key0 < kend && (!CAUSAL || key0 <= wpmax)) {
+                floatx16 s, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) { s[e] = 0.0f; dp[e] = 0.0f; }
+                const int arow = sub * 32 + pi32(l32);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    half8 a = *reinterpret_cast<const half8*>(sK[cur] + sw_off<DH>(arow, ks * 2 + lg));
+                    half8 c = *reinterpret_cast<const half8*>(sV[cur] + sw_off<DH>(arow, ks * 2 + lg));
+                    s = mfma32(a, qf[ks], s);
+                    dp = mfma32(c, gf[ks], dp);
+                }
+                const bool need_mask = (key0 + 32 > N) || (CAUSAL && key0 + 31 > wpmin) || !row_ok;
+                float ds[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float pe = exp2f(s[e] * p.scale_log2 - my_lse2);
+                    if (need_mask) {
+                        int key = key0 + 16 * (e >> 3) + 8 * lg + (e & 7);
+                        if (key >= N || (CAUSAL && key > qpos) || !row_ok) pe = 0.0f;
+                    }
+                    ds[e] = pe * (dp[e] - my_d);
+                }
+                const half8 b0 = pack8(&ds[0]), b1 = pack8(&ds[8]);
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+                    const int krow = t * 32 + l32;  // dh
+                    half8 a0 = *reinterpret_cast<const half8*>(sKt[cur] + sw_off<BC>(krow, sub * 4 + 0 + lg));
+                    half8 a1 = *reinterpret_cast<const half8*>(sKt[cur] + sw_off<BC>(krow, sub * 4 + 2 + lg));
+                    dq[t] = mfma32(a0, b0, dq[t]);
+                    dq[t] = mfma32(a1, b1, dq[t]);
+                }
+            }
+        }
+        if (more) {
+            lk.store(sK[cur ^ 1]); lv.store(sV[cur ^ 1]); lkt.store(sKt[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+    if (!row_ok) return;
+    f16* dQr = p.out + (int64_t)b * NH * DH + (int64_t)myrow * DH;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int dh = t * 32 + 8 * e4 + 4 * lg;
+            u32x2 w = {pack_h2(dq[t][4 * e4] * p.scale, dq[t][4 * e4 + 1] * p.scale),
+                       pack_h2(dq[t][4 * e4 + 2] * p.scale, dq[t][4 * e4 + 3] * p.scale)};
+            *reinterpret_cast<u32x2*>(dQr + dh) = w;
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Scalar fallbacks for head sizes without an MFMA kernel (any Dh <= 256).
+// One thread per query row (forward / stats / dQ) or per key (dK, dV).
+// ---------------------------------------------------------------------------
+constexpr int SC_MAXDH = 256;
+
+__global__ __launch_bounds__(64) void flash_fwd_scalar(FlashArgs p, int Dh, int causal, int mode) {
+    const int NH = p.N * p.H;
+    const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (idx >= (int64_t)p.B * NH) return;
+    const int b = (int)(idx / NH), r = (int)(idx % NH), pos = r / p.H, h = r % p.H;
+    const f16* qr = p.q + idx * Dh;
+    const f16* gr = mode ? p.dO + idx * Dh : nullptr;
+    float acc[SC_MAXDH];
+    for (int d = 0; d < Dh; ++d) acc[d] = 0.0f;
+    float m = -INFINITY, l = 0.0f, t = 0.0f;
+    const int L = causal ? pos + 1 : p.N;
+    for (int j = 0; j < L; ++j) {
+        const f16* kr = p.k + ((int64_t)b * p.N + j) * Dh;
+        const f16* vr = p.v + ((int64_t)b * p.N + j) * Dh;
+        float s = 0.0f, dpv = 0.0f;
+        for (int d = 0; d < Dh; ++d) {
+            s += (float)qr[d] * (float)kr[d];
+            if (mode) dpv += (float)gr[d] * (float)vr[d];
+        }
+        s *= p.scale_log2;
+        float mn = fmaxf(m, s);
+        float al = exp2f(m - mn), pe = exp2f(s - mn);
+        l = l * al + pe;
+        t = t * al + pe * dpv;
+        if (!mode)
+            for (int d = 0; d < Dh; ++d) acc[d] = acc[d] * al + pe * (float)vr[d];
+        m = mn;
+    }
+    const float il = l > 0.0f ? 1.0f / l : 0.0f;
+    if (!mode) {
+        for (int d = 0; d < Dh; ++d) p.out[idx * Dh + d] = (f16)(acc[d] * il);
+        if (p.lse) p.lse[((int64_t)b * p.H + h) * p.N + pos] = (m + log2f(l)) * kLn2;
+    } else {
+        p.lse2_rows[idx] = m + log2f(l);
+        p.d_rows[idx] = t * il;
+    }
+}
+
+__global__ __launch_bounds__(64) void flash_dq_scalar(FlashArgs p, int Dh, int causal) {
+    const int NH = p.N * p.H;
+    const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (idx >= (int64_t)p.B * NH) return;
+    const int b = (int)(idx / NH), r = (int)(idx % NH), pos = r / p.H;
+    const f16* qr = p.q + idx * Dh;
+    const f16* gr = p.dO + idx * Dh;
+    float acc[SC_MAXDH];
+    for (int d = 0; d < Dh; ++d) acc[d] = 0.0f;
+    const float l2 = p.lse2_rows[idx], Di = p.d_rows[idx];
+    const int L = causal ? pos + 1 : p.N;
+    for (int j = 0; j < L; ++j) {
+        const f16* kr = p.k + ((int64_t)b * p.N + j) * Dh;
+        const f16* vr = p.v + ((int64_t)b * p.N + j) * Dh;
+        float s = 0.0f, dpv = 0.0f;
+        for (int d = 0; d < Dh; ++d) {
+            s += (float)qr[d] * (float)kr[d];
+            dpv += (float)gr[d] * (float)vr[d];
+        }
+        float pe = exp2f(s * p.scale_log2 - l2);
+        float ds = pe * (dpv - Di);
+        for (int d = 0; d < Dh; ++d) acc[d] += ds * (float)kr[d];
+    }
+    for (int d = 0; d < Dh; ++d) p.out[idx * Dh + d] = (f16)(acc[d] * p.scale);
+}
+
+__global__ __launch_bounds__(64) void flash_dkdv_scalar(FlashArgs p, int Dh, int causal) {
+    const int NH = p.N * p.H;
+    const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (idx >= (int64_t)p.B * p.N) return;
+    const int b = (int)(idx / p.N), j = (int)(idx % p.N);
+    const f16* kr = p.k + idx * Dh;
+    const f16* vr = p.v + idx * Dh;
+    float ak[SC_MAXDH], av[SC_MAXDH];
+    for (int d = 0; d < Dh; ++d) { ak[d] = 0.0f; av[d] = 0.0f; }
+    const int rs = causal ? j * p.H : 0;
+    for (int r = rs; r < NH; ++r) {
+        const int64_t ri = (int64_t)b * NH + r;
+        const f16* qr = p.q + ri * Dh;
+        const f16* gr = p.dO + ri * Dh;
+        float s = 0.0f, dpv = 0.0f;
+        for (int d = 0; d < Dh; ++d) {
+            s += (float)qr[d] * (float)kr[d];
+            dpv += (float)gr[d] * (float)vr[d];
+        }
+        float pe = exp2f(s * p.scale_log2 - p.lse2_rows[ri]);
+        float ds = pe * (dpv - p.d_rows[ri]);
+        for (int d = 0; d < Dh; ++d) {
+            av[d] += pe * (float)gr[d];
+            ak[d] += ds * (float)qr[d];
+        }
+    }
+    for (int d = 0; d < Dh; ++d) {
+        p.dK[idx * Dh + d] = (f16)(ak[d] * p.scale);
+        p.dV[idx * Dh + d] = (f16)av[d];
+    }
+}
+
+__global__ __launch_bounds__(256) void flash_bwd_pre_scalar(FlashArgs p, int Dh) {
+    const int NH = p.N * p.H;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)p.B * NH) return;
+    const int b = (int)(idx / NH), r = (int)(idx % NH);
+    float acc = 0.0f;
+    for (int d = 0; d < Dh; ++d) acc += (float)p.o[idx * Dh + d] * (float)p.dO[idx * Dh + d];
+    p.d_rows[idx] = acc;
+    p.lse2_rows[idx] = p.lse[((int64_t)b * p.H + (r % p.H)) * p.N + r / p.H] * kLog2e;
+}
+
+// Workspace for the backward statistics (grow-only).
+float* g_bwd_ws = nullptr;
+size_t g_bwd_ws_elems = 0;
+
+template <int DH>
+hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st) {
+    dim3 grid((a.N * a.H + BR - 1) / BR, a.B);
+    if (mode == 0) {
+        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 0>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((flash_fwd<DH, false, 0>), grid, dim3(256), 0, st, a);
+    } else {
+        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 1>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((flash_fwd<DH, false, 1>), grid, dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int DH>
+hipError_t launch_bwd(const FlashArgs& a, bool causal, bool have_lse, hipStream_t st) {
+    const int NH = a.N * a.H;
+    if (have_lse) {
+        dim3 g((unsigned)(((int64_t)a.B * NH + 255) / 256));
+        hipLaunchKernelGGL(flash_bwd_pre<DH>, g, dim3(256), 0, st, a);
+    } else {
+        hipError_t e = launch_fwd<DH>(a, causal, 1, st);
+        if (e != hipSuccess) return e;
+    }
+    dim3 gk((a.N + 31) / 32, a.B);
+    dim3 gq((NH + BR - 1) / BR, a.B);
+    if (causal) {
+        hipLaunchKernelGGL((flash_bwd_dkdv<DH, true>), gk, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((flash_bwd_dq<DH, true>), gq, dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_dkdv<DH, false>), gk, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((flash_bwd_dq<DH, false>), gq, dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+void flash_free_workspace() {
+    if (g_bwd_ws) (void)hipFree(g_bwd_ws);
+    g_bwd_ws = nullptr;
+    g_bwd_ws_elems = 0;
+}
+
+int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
+    a.scale = 1.0f / sqrtf((float)dh);
+    a.scale_log2 = a.scale * kLog2e;
+    hipError_t e;
+    if (mfma && dh == 32) e = launch_fwd<32>(a, causal, 0, st);
+    else if (mfma && dh == 64) e = launch_fwd<64>(a, causal, 0, st);
+    else if (mfma && dh == 128) e = launch_fwd<128>(a, causal, 0, st);
+    else {
+        dim3 g((unsigned)(((int64_t)a.B * a.N * a.H + 63) / 64));
+        hipLaunchKernelGGL(flash_fwd_scalar, g, dim3(64), 0, st, a, dh, (int)causal, 0);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? EVKHIP_OK : check_hip(e, "flash forward launch");
+}
+
+int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
+    a.scale = 1.0f / sqrtf((float)dh);
+    a.scale_log2 = a.scale * kLog2e;
+    const size_t rows = (size_t)a.B * a.N * a.H;
+    if (2 * rows > g_bwd_ws_elems) {
+        if (g_bwd_ws) EVK_HIP(hipFree(g_bwd_ws));
+        g_bwd_ws = nullptr;
+        EVK_HIP(hipMalloc(&g_bwd_ws, 2 * rows * sizeof(float)));
+        g_bwd_ws_elems = 2 * rows;
+    }
+    a.lse2_rows = g_bwd_ws;
+    a.d_rows = g_bwd_ws + rows;
+    const bool have_lse = a.lse != nullptr;
+    hipError_t e;
+    if (mfma && dh == 32) e = launch_bwd<32>(a, causal, have_lse, st);
+    else if (mfma && dh == 64) e = launch_bwd<64>(a, causal, have_lse, st);
+    else if (mfma && dh == 128) e = launch_bwd<128>(a, causal, have_lse, st);
+    else {
+        dim3 g((unsigned)((rows + 63) / 64));
+        if (have_lse) {
+            hipLaunchKernelGGL(flash_bwd_pre_scalar, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                               a, dh);
+        } else {
+            hipLaunchKernelGGL(flash_fwd_scalar, g, dim3(64), 0, st, a, dh, (int)causal, 1);
+        }
+        hipLaunchKernelGGL(flash_dq_scalar, g, dim3(64), 0, st, a, dh, (int)causal);
+        dim3 gk((unsigned)(((int64_t)a.B * a.N + 63) / 64));
+        hipLaunchKernelGGL(flash_dkdv_scalar, gk, dim3(64), 0, st, a, dh, (int)causal);
+        e = hipGetLastError();
+    }
+    return e == hipSuccess ? EVKHIP_OK : check_hip(e, "flash backward launch");
+}
+
+}  // namespace evkhip

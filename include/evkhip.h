@@ -1,0 +1,173 @@
+/*
+ * evkhip.h - C ABI of the MI355X (gfx950) kernel library behind evk::ai.
+ *
+ * This is the drop-in boundary: the evk::ai C++ API (include/evk_ai.h) keeps
+ * the reference's signatures and calls these entry points instead of
+ * recording Vulkan dispatches of the reference's SPIR-V compute shaders.
+ *
+ * Conventions
+ *   - Every tensor is described by an evkhip_tensor: a device pointer plus the
+ *     shape (row-major, contiguous).  Elements are IEEE binary16 unless the
+ *     entry point says otherwise (token ids are raw uint16 in fp16 storage, as
+ *     in the reference, evk_ai.h:560-566).
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Entry points only
+ *     enqueue work; ordering follows the stream, which reproduces the full
+ *     barrier the reference records after every op (evk_ai.cpp:329 etc.).
+ *   - Return value: EVKHIP_OK (0) or a negative EVKHIP_ERR_* code; the message
+ *     of the last failure on the calling thread is evkhip_last_error().
+ *   - Shape and argument validation happens on the host before any HIP call,
+ *     so it can be exercised without a GPU.
+ *   - Not thread-safe across concurrent calls that share library workspace
+ *     (the reference is single-threaded with global state, evk_ai.cpp:4,63).
+ */
+#ifndef EVKHIP_H
+#define EVKHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EVKHIP_MAX_DIMS 8
+
+enum {
+    EVKHIP_OK = 0,
+    EVKHIP_ERR_INVALID_ARG = -1, /* null pointer, bad flag, inconsistent sizes */
+    EVKHIP_ERR_SHAPE = -2,       /* shapes violate the op's contract            */
+    EVKHIP_ERR_UNSUPPORTED = -3, /* valid request this build does not implement */
+    EVKHIP_ERR_HIP = -4,         /* a HIP runtime call failed                   */
+    EVKHIP_ERR_ALLOC = -5        /* workspace allocation failed                 */
+};
+
+typedef struct evkhip_tensor {
+    void* data;                       /* device pointer                    */
+    uint32_t rank;                    /* 1..EVKHIP_MAX_DIMS                */
+    uint32_t dims[EVKHIP_MAX_DIMS];   /* dims[0] outermost                 */
+} evkhip_tensor;
+
+/* Library version string, e.g. "evkhip 0.1 gfx950". */
+const char* evkhip_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* evkhip_last_error(void);
+
+/* Replaces evk::ai::initialize (evk_ai.cpp:211-246): no pipelines to build;
+ * records the current device.  Optional: every entry point works without it. */
+int evkhip_init(void);
+
+/* Replaces evk::ai::shutdown (evk_ai.cpp:248-252): frees library workspace
+ * (the grow-only flash scratch, cf. evk_ai.cpp:135-157). */
+int evkhip_shutdown(void);
+
+/* evk::ai::matmul (evk_ai.h:495, evk_ai.cpp:254-330).
+ * C[b] (+)= op(A[b]) . op(B[b]):  A (...,M,K) or (...,K,M) if transpose_a;
+ * B (...,K,N) or (...,N,K) if transpose_b; C (...,M,N).  batch = max of the
+ * operands' leading-dim products; an input with batch 1 broadcasts.  fp32
+ * accumulation, fp16 output; acc_c adds the prior C.  tile_m/tile_n are the
+ * reference's tile hints: accepted (and validated as multiples of 16 when
+ * nonzero) but the kernel picks its own MFMA tiling, and M, N, K need not be
+ * multiples of them. */
+int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c,
+                  int transpose_a, int transpose_b, int acc_c,
+                  uint32_t tile_m, uint32_t tile_n, void* stream);
+
+/* evk::ai::flash_attention (evk_ai.h:497-501, evk_ai.cpp:332-369).
+ * MQA: Q,O (B,N,H*Dh); K,V (B,N,Dh); H = D/Dh; scale 1/sqrt(Dh).
+ * Extensions (defaults reproduce the reference): causal != 0 masks keys
+ * j > i; lse, if non-NULL, receives the fp32 log-sum-exp of every (b,h,i)
+ * row, laid out (B,H,N).  Dh in {16,32,64,128}. */
+int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k,
+                           const evkhip_tensor* v, const evkhip_tensor* o,
+                           int causal, float* lse, void* stream);
+
+/* evk::ai::flash_attention_bwd (evk_ai.h:503, evk_ai.cpp:371-473).
+ * dQ (B,N,D); dK,dV (B,N,Dh) summed over the H heads sharing them.
+ * heads != 0 must equal D/Dh.  With lse == NULL the row statistics and
+ * D_i = sum_j P_ij dP_ij are recomputed from Q,K,V,dO and `o` is not read
+ * (the reference never reads it either); with lse from the forward pass,
+ * D_i = rowsum(dO_i * O_i) is taken from `o` and the recompute is skipped.
+ * Uses library workspace (grow-only, freed by evkhip_shutdown). */
+int evkhip_flash_attention_bwd(const evkhip_tensor* q, const evkhip_tensor* k,
+                               const evkhip_tensor* v, const evkhip_tensor* o,
+                               const evkhip_tensor* dO, const evkhip_tensor* dQ,
+                               const evkhip_tensor* dK, const evkhip_tensor* dV,
+                               uint32_t heads, int causal, const float* lse, void* stream);
+
+/* Decode-step attention: the host entry that single_query_attention.comp
+ * (lines 26-72) never had.  q (heads*dh) or (1,1,heads*dh); k_cache, v_cache
+ * (...,max_len,heads*dh) row-major; attends over cache rows
+ * [0,current_length).  heads == 1, dh <= 64, current_length <= 160 is the
+ * shader's contract; this entry lifts those limits (split-K with a merge). */
+int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k_cache,
+                                  const evkhip_tensor* v_cache, const evkhip_tensor* out,
+                                  uint32_t current_length, uint32_t heads, void* stream);
+
+/* evk::ai::rms_norm (evk_ai.h:610, evk_ai.cpp:1045-1067, rms_norm.comp). */
+int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream);
+
+/* evk::ai::rope (evk_ai.h:589-591, evk_ai.cpp:945-966, rope.comp).
+ * Extensions (0 reproduces the reference): position t = position_offset +
+ * sequence index; head_dim splits embed_dim into independently rotated heads
+ * whose frequencies use head_dim (0 means embed_dim). */
+int evkhip_rope(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t batch_size,
+                uint32_t seq_len, uint32_t embed_dim, float rotary_base,
+                uint32_t position_offset, uint32_t head_dim, void* stream);
+
+/* evk::ai::gelu (evk_ai.h:540, evk_ai.cpp:679-699, gelu.comp). */
+int evkhip_gelu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream);
+
+/* evk::ai::add (evk_ai.h:521, evk_ai.cpp:568-591, add.comp). */
+int evkhip_add(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c,
+               void* stream);
+
+/* evk::ai::embed (evk_ai.h:558, evk_ai.cpp:782-806, embed.comp).
+ * Indices are raw uint16 ids; ids >= vocab are clamped to vocab-1. */
+int evkhip_embed(const evkhip_tensor* embeddings, const evkhip_tensor* indices,
+                 const evkhip_tensor* out, void* stream);
+
+/* evk::ai::greedy_sample (evk_ai.h:563-566, evk_ai.cpp:808-837,
+ * greedy_sample.comp).  Same winner as the shader, including its tie order. */
+int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out_tokens,
+                         uint32_t position, uint16_t token_base, uint16_t token_count,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * KV-cached greedy decode (the caller the single-query path exists for; the
+ * reference decodes by full recompute, example/main_llm.cpp:622-654).  The
+ * model is the reference block (main_llm.cpp:528-546) in multi-head,
+ * KV-cached form.  Weights: one fp16 blob laid out
+ *   E (vocab,d); per layer Wqkv (d,3d) [q|k|v], Wo (d,d), W1 (d,hidden),
+ *   W2 (hidden,d); Wout (d,vocab)
+ * Cache: per layer K (max_seq,d) then V (max_seq,d).
+ * ------------------------------------------------------------------------- */
+typedef struct evkhip_model_cfg {
+    uint32_t vocab, d, heads, dh, layers, hidden, max_seq;
+    float eps, rope_base;
+} evkhip_model_cfg;
+
+/* Elements (fp16) of the weight blob / the KV cache for `cfg`. */
+uint64_t evkhip_model_weight_elems(const evkhip_model_cfg* cfg);
+uint64_t evkhip_model_cache_elems(const evkhip_model_cfg* cfg);
+
+/* Prefill: runs prompt tokens[0..n_tokens) (device, uint16) at positions
+ * pos0.. through the model, appending to the cache; then writes the last
+ * position's logits (device, fp16 vocab) and its greedy id to next_id[0]
+ * (device uint16).  Workspace is library-owned. */
+int evkhip_model_prefill(const evkhip_model_cfg* cfg, const void* weights, void* cache,
+                         const uint16_t* tokens, uint32_t n_tokens, uint32_t pos0,
+                         uint16_t* next_id, void* logits, void* stream);
+
+/* Greedy decode: token_io (device, uint16, n_steps+1 entries).  Step s feeds
+ * token_io[s] at position pos0+s and writes its greedy id to token_io[s+1],
+ * which the next step's embedding reads on the device (no host round trip).
+ * logits (device, fp16 vocab) holds the last step's logits. */
+int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* cache,
+                        uint16_t* token_io, uint32_t n_steps, uint32_t pos0, void* logits,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EVKHIP_H */
