@@ -1,0 +1,236 @@
+"""Benchmark of the evk AI hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+
+Headline: causal MQA flash-attention forward,
+fp16, B=4, H=8, S=1024, Dh=64, inputs resident in HBM.  A step is one
+evk::ai::flash_attention call over the whole batch (one kernel launch);
+TFLOP/s uses the causal convention 2*B*H*S^2*Dh = 4.295 GFLOP per step.
+`roofline` compares the kernel's achieved TFLOP/s with MI355X's dense fp16
+MFMA peak; `traffic` is the HBM bytes per launch measured with rocprofv3
+(FETCH_SIZE + WRITE_SIZE, profiles/flash_fwd_c2_traffic.txt) when present.
+`cpu_baseline` times the CPU oracle's restatement of the same attention on
+the host (single thread) on the same workload.
+
+The other configurations of BASELINE.json are reported under "secondary"
+(same JSON line): GEMM 1024^3, 4096^3, QKV 8192x12288x4096, skinny GEMV
+M in {1,4,16} x 11008 x 4096, causal flash backward (C3), and the C4 greedy
+decode (tokens/s over 32 steps and algorithmic GB/s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+METRIC = "fp16 GEMM & flash-attn fwd/bwd TFLOP/s (% MFMA peak); decode tok/s, GB/s"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-extras", action="store_true", help="headline only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", default="", help="comma list of secondary workloads to run")
+    p.add_argument("--profile-copy", action="store_true",
+                   help="only run a plain 64 MiB device-to-device copy (HBM counter calibration)")
+    return p.parse_args()
+
+
+def profile_copy():
+    """Plain copy of a known size: the reference point that scales rocprofv3's
+    FETCH_SIZE / WRITE_SIZE readings into HBM bytes."""
+    import torch
+    n = 64 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copied {n} bytes x 20")
+
+
+def timed(fn, steps, warmup):
+    """Average ms per call of fn() over `steps` back-to-back calls on torch's
+    current stream (the stream the kernels are launched on), HIP events."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].split()[0])
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the evk hot path is single-device; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.profile_copy:
+        profile_copy()
+        return
+    import numpy as np
+    import torch
+
+    import evk_amd as evk
+    import oracle as orc
+
+    dev = torch.device("cuda:0")
+    evk.initialize()
+
+    def to_dev(x):
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.float16).to(dev)
+
+    # ---------------- headline: C2 causal flash forward -------------------
+    B, H, S, Dh = 4, 8, 1024, 64
+    q = orc.normal_f16((B, S, H * Dh), 201)
+    k = orc.normal_f16((B, S, Dh), 202)
+    v = orc.normal_f16((B, S, Dh), 203)
+    Q, K, V = to_dev(q), to_dev(k), to_dev(v)
+    O = torch.empty_like(Q)
+    L = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    flops = 2.0 * B * H * S * S * Dh
+    torch.cuda.synchronize()
+    ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    traffic = read_traffic("flash_fwd_c2_traffic.txt")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) fp16)",
+        "config": {"workload": "causal MQA flash-attention forward (BASELINE configs[1])",
+                   "B": B, "H": H, "S": S, "head_dim": Dh, "kv_heads": 1,
+                   "flop_convention": "2*B*H*S^2*Dh (causal)", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+                     "traffic": traffic},
+    }
+
+    # ---------------- secondary configurations ---------------------------
+    sec = {}
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not args.no_extras and (not only or name in only)
+
+    def gemm(gm, gn, gk, seed, steps):
+        a = to_dev(orc.uniform_f16((gm, gk), seed))
+        b = to_dev(orc.uniform_f16((gk, gn), seed + 1))
+        c = torch.empty((gm, gn), dtype=torch.float16, device=dev)
+        ms_ = timed(lambda: evk.matmul(a, b, c), steps, 5)
+        del a, b, c
+        return ms_
+
+    if want("gemm"):
+        for name, (gm, gn, gk, st) in {"gemm_1024": (1024, 1024, 1024, 200),
+                                       "gemm_4096": (4096, 4096, 4096, 30),
+                                       "gemm_qkv_8192x12288x4096": (8192, 12288, 4096, 10)}.items():
+            ms_ = gemm(gm, gn, gk, 101, st)
+            tf = 2.0 * gm * gn * gk / (ms_ * 1e-3) / 1e12
+            sec[name] = {"ms": round(ms_, 4), "TFLOP/s": round(tf, 1),
+                         "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+    if want("gemv"):
+        for gm in (1, 4, 16):
+            ms_ = gemm(gm, 11008, 4096, 501, 200)
+            gbs = (4096 * 11008 + gm * 4096 + gm * 11008) * 2 / (ms_ * 1e-3) / 1e9
+            sec[f"gemv_m{gm}_11008x4096"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
+                                            "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    if want("flash_bwd"):
+        G = to_dev(orc.normal_f16((B, S, H * Dh), 204))
+        dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+        evk.flash_attention(Q, K, V, O, causal=True, lse=L)
+        ms_ = timed(lambda: evk.flash_attention_bwd(Q, K, V, O, G, dQ, dK, dV, causal=True, lse=L),
+                    100, 10)
+        tf = 2.5 * flops / (ms_ * 1e-3) / 1e12
+        sec["flash_bwd_c3"] = {"ms": round(ms_, 4), "TFLOP/s": round(tf, 1),
+                               "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4),
+                               "flop_convention": "5*B*H*S^2*Dh (2.5x forward)"}
+    if want("decode"):
+        cfg = evk.model_cfg()
+        ocfg = orc.model_cfg()
+        w = to_dev(orc.model_weights(ocfg, seed=301, std=0.02))
+        prompt = torch.from_numpy(orc.tokens_u16(1024, 302, 32000).view(np.int16)).to(dev)
+        cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
+        tok = torch.zeros(33, dtype=torch.int16, device=dev)
+        logits = torch.empty(cfg.vocab, dtype=torch.float16, device=dev)
+        evk.model_prefill(cfg, w, cache, prompt, 0, tok, logits)
+        torch.cuda.synchronize()
+        first = tok[0].clone()
+
+        def run32():
+            tok[0] = first  # same 32 steps every repetition (positions 1024..1055)
+            evk.model_decode(cfg, w, cache, tok, 32, 1024, logits)
+
+        ms32 = timed(run32, 5, 1)
+        d, hid, V_ = 768, 3072, 32000
+        layer_bytes = 12 * (d * 3 * d + d * d + 2 * d * hid) * 2
+        kv_bytes = sum(12 * 2 * (1024 + s + 1) * d * 2 for s in range(32)) / 32
+        step_bytes = layer_bytes + d * V_ * 2 + kv_bytes
+        tok_s = 32 / (ms32 * 1e-3)
+        gbs = step_bytes * tok_s / 1e9
+        sec["decode_c4"] = {"ms_per_token": round(ms32 / 32, 4), "tokens/s": round(tok_s, 1),
+                            "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                            "bytes_per_token": int(step_bytes)}
+        del w, cache
+    if sec:
+        out["secondary"] = sec
+
+    # ---------------- CPU baseline (oracle port, single thread) ----------
+    if not args.no_cpu:
+        lib = orc.lib()
+        lib.orc_set_threads(1)
+        t0 = time.perf_counter()
+        orc.attention_fwd(q, k, v, True)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+                               "kind": "port",
+                               "sample": "the full C2 workload (B=4,H=8,S=1024,Dh=64 causal) through "
+                                         "oracle/oracle.c orc_attention_fwd, fp32, one thread, "
+                                         f"{dt:.1f} s"}
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -39,9 +39,17 @@ def _run(cmd):
     return r
 
 
+# Files whose MFMA accumulators fit in the architectural VGPRs: keep them there
+# (no AGPR<->VGPR copies around the softmax / epilogue arithmetic).
+VGPR_MFMA = {"flash.hip"}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    # flash.hip never produces NaNs on purpose (masked scores are -inf), so
+    # max trees need no NaN-quieting copies
+    extra = ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"] if src in VGPR_MFMA else []
+    cmd = [HIPCC] + HIP_FLAGS + extra + ["-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC, "-x", "hip"] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
     _run(cmd)

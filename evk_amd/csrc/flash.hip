@@ -123,179 +123,312 @@ DEV half8 pack8v(const floatx16& x, int off) {
 // ---------------------------------------------------------------------------
 // Forward (MODE 0: O and public LSE) / statistics for the backward (MODE 1:
 // lse2_rows and d_rows, with dP^T = V dO^T in place of the PV product).
-// Grid: (ceil(N*H/128), B); 256 threads.
+//
+// Workgroup: 4 waves x 16 query rows (64 rows) sharing row-major K and V
+// tiles of 64 keys in LDS (double-buffered, rows padded by 32 bytes).  Each
+// wave uses v_mfma_f32_16x16x32_f16:
+//   S^T(16 keys x 16 q) = K(16 x 32dh) Q^T: lane l holds query l%16 and keys
+//       4*(l/16)+j of each 16-key tile.
+//   O^T(16 dh x 16 q) += V^T(16 dh x 32 keys) P^T: the probabilities already
+//       sit in B-operand order (slot s <-> key 4*(l/16)+s of the first and
+//       second 16-key tile), and V^T comes straight from the row-major V tile
+//       through ds_read_tr16_b64 (4 consecutive key rows of one dh column per
+//       lane).
+// The softmax scale*log2(e) is folded into one FMA before v_exp_f32; the
+// O rescale is skipped when no row maximum of the wave moved.
+// Grid: ceil(N*H/64) * B workgroups; causal grids run heaviest rows first,
+// in a zigzag so that the pairs of workgroups that share a CU carry about the
+// same number of key tiles.
 // ---------------------------------------------------------------------------
+constexpr int FR = 64;  // query rows per workgroup (4 waves x 16)
+constexpr int KT = 64;  // keys per LDS tile
+
+DEV floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+// 4 consecutive rows of one column of a row-major 16-bit LDS tile
+// (ds_read_b64_tr_b16); `p` is this lane's address as described above.
+DEV half4 lds_read_tr(const f16* p) {
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (__attribute__((address_space(3))) fp16x4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+DEV half8 cat4(const half4& a, const half4& b) {
+    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Maps a linear workgroup id to (row group, batch).  Causal: heaviest row
+// groups first, alternate rounds of `round` groups reversed.
+DEV void fwd_block_map(int bid, int nrg, int B, bool causal, int round, int* rg, int* b) {
+    const int total = nrg * B;
+    int idx = bid;
+    if (causal) {
+        const int r = bid / round, pos = bid % round;
+        const int base = r * round;
+        const int len = min(round, total - base);
+        idx = (r & 1) ? base + (len - 1 - pos) : bid;
+        *rg = nrg - 1 - idx / B;
+    } else {
+        *rg = idx / B;
+    }
+    *b = idx % B;
+}
+
+// Lazy rescaling: a wave keeps a reference maximum m_ref per query row and
+// only re-normalises (O, l scaled by 2^(m_old-m_new)) when some score exceeds
+// m_ref by more than 2^RESCALE_LOG2; in between, probabilities are
+// 2^(s*c - m_ref) <= 2^RESCALE_LOG2, exact enough in fp16 and fp32 sums.
+constexpr float RESCALE_LOG2 = 8.0f;
+
 template <int DH, bool CAUSAL, int MODE>
-__global__ __launch_bounds__(256) void flash_fwd(FlashArgs p) {
-    constexpr int KS = DH / 16;  // k-steps of the QK^T contraction
-    constexpr int DT = DH / 32;  // 32-row dh tiles of O^T
-    __shared__ __attribute__((aligned(16))) f16 sK[2][BC * DH];
-    __shared__ __attribute__((aligned(16))) f16 sV[2][BC * DH];  // MODE 0: V^T [DH][BC]; MODE 1: V [BC][DH]
+__global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
+    constexpr int KS = DH / 32;   // k-steps of QK^T (32 dh each)
+    constexpr int DT = DH / 16;   // 16-row dh tiles of O^T
+    constexpr int LW = DH + 8;    // LDS row stride in halves (16-byte pad)
+    constexpr int TILE = KT * LW; // halves per K (or V) tile
+    constexpr int CH = KT * DH / 8;  // 16-byte chunks per tile
+    constexpr int PER = (CH + 255) / 256;
+    // [stage][half][K tile, V tile]: the two wave sets take alternate tiles
+    __shared__ __attribute__((aligned(16))) f16 smem[2 * 2 * 2 * TILE];
 
     const int H = p.H, N = p.N, NH = N * H;
-    const int b = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int l32 = lane & 31, lg = lane >> 5;
-    const int R0 = blockIdx.x * BR;
-    const int rw0 = R0 + wave * 32;                // first row of this wave
-    const int myrow = rw0 + l32;                   // the query row of this lane
+    const int nrg = (NH + FR - 1) / FR;
+    int rg, b;
+    fwd_block_map(blockIdx.x, nrg, p.B, CAUSAL, round, &rg, &b);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int rw = wave & 3, half = wave >> 2;   // row wave, key half
+    const int tid = threadIdx.x & 255;           // index within the half
+    const int l16 = lane & 15, g = lane >> 4;
+    const int R0 = rg * FR;
+    const int rw0 = R0 + rw * 16;
+    const int myrow = rw0 + l16;
     const bool row_ok = myrow < NH;
     const int qpos = min(myrow, NH - 1) / H;
-    const int wpmax = min(rw0 + 31, NH - 1) / H;   // largest position in the wave
+    const int wpmax = min(rw0 + 15, NH - 1) / H;
     const int wpmin = min(rw0, NH - 1) / H;
-    const int bpmax = min(R0 + BR - 1, NH - 1) / H;
+    const int bpmax = min(R0 + FR - 1, NH - 1) / H;
     const int kend = CAUSAL ? min(N, bpmax + 1) : N;
+    const float c2 = p.scale_log2;
 
     const f16* Qb = p.q + (int64_t)b * NH * DH;
     const f16* Kb = p.k + (int64_t)b * N * DH;
     const f16* Vb = p.v + (int64_t)b * N * DH;
 
-    // Q^T fragments (B operand): lane holds row myrow, dh [16ks + 8lg, +8).
-    half8 qf[KS];
-    half8 dof[KS];
+    // B operand of S^T: lane holds query row myrow, dh [32ks + 8g, +8)
+    half8 qf[KS], gf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (row_ok) v = *reinterpret_cast<const u32x4*>(Qb + (int64_t)myrow * DH + ks * 16 + lg * 8);
-        qf[ks] = as_half8(v);
-        if constexpr (MODE == 1) {
-            u32x4 w = {0u, 0u, 0u, 0u};
-            if (row_ok)
+        u32x4 v = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
+        if (row_ok) {
+            v = *reinterpret_cast<const u32x4*>(Qb + (int64_t)myrow * DH + ks * 32 + g * 8);
+            if constexpr (MODE == 1)
                 w = *reinterpret_cast<const u32x4*>(p.dO + (int64_t)b * NH * DH + (int64_t)myrow * DH +
-                                                    ks * 16 + lg * 8);
-            dof[ks] = as_half8(w);
+                                                    ks * 32 + g * 8);
         }
+        qf[ks] = as_half8(v);
+        gf[ks] = as_half8(w);
     }
+    // Drain the Q loads now: the main loop then only ever waits for the K/V
+    // prefetch at the LDS store, never at the first MFMA of a tile.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
-    floatx16 oacc[DT];
+    floatx4 oacc[DT];
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+    for (int d = 0; d < DT; ++d) oacc[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_ref = -INFINITY, t_part = 0.0f;
+    floatx4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};  // row sums (all 4 elements equal)
+    const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f,
+                         (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
+
+    // Each half stages its own tile (key tiles 2i and 2i+1 of pair i).
+    // Rows past N load row N-1: those keys are masked to p = 0.
+    u32x4 rr[2 * PER];
+    auto gload = [&](int key0) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[t][e] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f, t_run = 0.0f;
+        for (int i = 0; i < PER; ++i) {
+            const int c = min(tid + i * 256, CH - 1);
+            const int row = min(key0 + c / (DH / 8), N - 1), ch = c % (DH / 8);
+            rr[i] = *reinterpret_cast<const u32x4*>(Kb + (int64_t)row * DH + ch * 8);
+            rr[PER + i] = *reinterpret_cast<const u32x4*>(Vb + (int64_t)row * DH + ch * 8);
+        }
+    };
+    auto lstore = [&](int stage) {
+        f16* kb = smem + ((stage * 2 + half) * 2) * TILE;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = tid + i * 256;
+            if (CH % 256 == 0 || c < CH) {
+                const int row = c / (DH / 8), ch = c % (DH / 8);
+                *reinterpret_cast<u32x4*>(kb + row * LW + ch * 8) = rr[i];
+                *reinterpret_cast<u32x4*>(kb + TILE + row * LW + ch * 8) = rr[PER + i];
+            }
+        }
+    };
 
-    RowTile<BC, DH, 256> lk;
-    RowTile<BC, DH, 256> lv_rows;    // MODE 1
-    TransTile<BC, DH, 256> lv_t;     // MODE 0
-
-    const int nkt = (kend + BC - 1) / BC;
-    if (nkt > 0) {
-        lk.load(Kb, 0, N);
-        if constexpr (MODE == 0) lv_t.load(Vb, 0, N); else lv_rows.load(Vb, 0, N);
-        lk.store(sK[0]);
-        if constexpr (MODE == 0) lv_t.store(sV[0]); else lv_rows.store(sV[0]);
+    const int nkt = (kend + KT - 1) / KT;
+    const int npair = (nkt + 1) / 2;
+    if (npair > 0) {
+        if (2 * 0 + half < nkt) gload(half * KT);
+        lstore(0);
+        if (npair > 1 && 2 + half < nkt) gload((2 + half) * KT);
     }
     __syncthreads();
 
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nkt;
-        if (more) {
-            lk.load(Kb, (kt + 1) * BC, N);
-            if constexpr (MODE == 0) lv_t.load(Vb, (kt + 1) * BC, N); else lv_rows.load(Vb, (kt + 1) * BC, N);
-        }
-        const f16* ks_ = sK[cur];
-        const f16* vs_ = sV[cur];
+    for (int pi = 0; pi < npair; ++pi) {
+        const int stage = pi & 1;
+        const int kt = 2 * pi + half;
+        const int key0 = kt * KT;
+        if (kt < nkt && (!CAUSAL || key0 <= wpmax)) {
+            const f16* ks_ = smem + ((stage * 2 + half) * 2) * TILE;
+            const f16* vs_ = ks_ + TILE;
+            floatx4 s[4];
 #pragma unroll
-        for (int sub = 0; sub < BC / 32; ++sub) {
-            const int key0 = kt * BC + sub * 32;
-            if (key0 < kend && (!CAUSAL || key0 <= wpmax)) {
-                floatx16 s;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) s[e] = 0.0f;
-                const int arow = sub * 32 + pi32(l32);
+            for (int t = 0; t < 4; ++t) {
+                s[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    half8 a = *reinterpret_cast<const half8*>(ks_ + sw_off<DH>(arow, ks * 2 + lg));
-                    s = mfma32(a, qf[ks], s);
+                    half8 a = *reinterpret_cast<const half8*>(ks_ + (t * 16 + l16) * LW + ks * 32 + g * 8);
+                    s[t] = mfma16(a, qf[ks], s[t]);
                 }
-                floatx16 dp;
-                if constexpr (MODE == 1) {
+            }
+            floatx4 dp[4];
+            if constexpr (MODE == 1) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) dp[e] = 0.0f;
+                for (int t = 0; t < 4; ++t) {
+                    dp[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks) {
-                        half8 a = *reinterpret_cast<const half8*>(vs_ + sw_off<DH>(arow, ks * 2 + lg));
-                        dp = mfma32(a, dof[ks], dp);
-                    }
-                }
-                // element e holds key key0 + 16*(e/8) + 8*lg + e%8
-                const bool need_mask = (key0 + 32 > N) || (CAUSAL && key0 + 31 > wpmin);
-                float mloc = -INFINITY;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    float v = s[e] * p.scale_log2;
-                    if (need_mask) {
-                        int key = key0 + 16 * (e >> 3) + 8 * lg + (e & 7);
-                        if (key >= N || (CAUSAL && key > qpos)) v = -INFINITY;
-                    }
-                    s[e] = v;
-                    mloc = fmaxf(mloc, v);
-                }
-                mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-                const float m_new = fmaxf(m_run, mloc);
-                const float base = (m_new == -INFINITY) ? 0.0f : m_new;
-                const float alpha = exp2f(m_run - base);
-                float psum = 0.0f, tsum = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    float pe = exp2f(s[e] - base);
-                    s[e] = pe;
-                    psum += pe;
-                    if constexpr (MODE == 1) tsum += pe * dp[e];
-                }
-                l_run = l_run * alpha + psum;
-                m_run = m_new;
-                if constexpr (MODE == 1) {
-                    t_run = t_run * alpha + tsum;
-                } else {
-                    half8 pb0 = pack8v(s, 0);
-                    half8 pb1 = pack8v(s, 8);
-#pragma unroll
-                    for (int t = 0; t < DT; ++t) {
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
-                        const int vrow = t * 32 + l32;  // dh
-                        half8 a0 = *reinterpret_cast<const half8*>(vs_ + sw_off<BC>(vrow, sub * 4 + 0 + lg));
-                        half8 a1 = *reinterpret_cast<const half8*>(vs_ + sw_off<BC>(vrow, sub * 4 + 2 + lg));
-                        oacc[t] = mfma32(a0, pb0, oacc[t]);
-                        oacc[t] = mfma32(a1, pb1, oacc[t]);
+                        half8 a = *reinterpret_cast<const half8*>(vs_ + (t * 16 + l16) * LW + ks * 32 + g * 8);
+                        dp[t] = mfma16(a, gf[ks], dp[t]);
                     }
                 }
             }
+            // element j of s[t]: key key0 + 16t + 4g + j (raw, unscaled scores)
+            if ((key0 + KT > N) || (CAUSAL && key0 + KT - 1 > wpmin)) {
+                const int lim = (CAUSAL ? min(N - 1, qpos) : N - 1) - key0 - 4 * g;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) s[t][j] = (t * 16 + j > lim) ? -INFINITY : s[t][j];
+            }
+            float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                             fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[2][0], s[2][1]), fmaxf(s[2][2], s[2][3])),
+                                 fmaxf(fmaxf(s[3][0], s[3][1]), fmaxf(s[3][2], s[3][3]))));
+            mx *= c2;
+            if (__any(mx > m_ref + RESCALE_LOG2)) {
+                // new reference: the exact row maximum across the 4 lane groups
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m_ref, mx);
+                const float alpha = (m_ref == -INFINITY) ? 0.0f : fast_exp2(m_ref - m_new);
+#pragma unroll
+                for (int d = 0; d < DT; ++d) oacc[d] *= alpha;
+                lacc *= alpha;
+                t_part *= alpha;
+                m_ref = m_new;
+            }
+            const float nbase = (m_ref == -INFINITY) ? 0.0f : -m_ref;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float pe = fast_exp2(__builtin_fmaf(s[t][j], c2, nbase));
+                    if constexpr (MODE == 1) t_part += pe * dp[t][j];
+                    s[t][j] = pe;
+                }
+            // P^T as B operands: k-step kk covers tiles 2kk, 2kk+1
+            half8 pb[2];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                u32x4 u = {pack_h2(s[2 * kk][0], s[2 * kk][1]), pack_h2(s[2 * kk][2], s[2 * kk][3]),
+                           pack_h2(s[2 * kk + 1][0], s[2 * kk + 1][1]),
+                           pack_h2(s[2 * kk + 1][2], s[2 * kk + 1][3])};
+                pb[kk] = as_half8(u);
+            }
+            // row sums of the fp16 probabilities on the MFMA: ones(16x32) . P^T
+            // leaves the full sum over the tile's keys in every element
+            lacc = mfma16(ones8, pb[0], lacc);
+            lacc = mfma16(ones8, pb[1], lacc);
+            if constexpr (MODE == 0) {
+                // this lane's ds_read_tr address within a 4-row x 16-col block
+                const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) {
+                        const f16* base0 = vs_ + (kk * 32 + g * 4 + trow) * LW + d * 16 + tcol;
+                        half4 lo = lds_read_tr(base0);
+                        half4 hi = lds_read_tr(base0 + 16 * LW);
+                        oacc[d] = mfma16(cat4(lo, hi), pb[kk], oacc[d]);
+                    }
+            }
         }
-        if (more) {
-            lk.store(sK[cur ^ 1]);
-            if constexpr (MODE == 0) lv_t.store(sV[cur ^ 1]); else lv_rows.store(sV[cur ^ 1]);
+        if (pi + 1 < npair) {
+            if (2 * (pi + 1) + half < nkt) lstore(stage ^ 1);
+            if (pi + 2 < npair && 2 * (pi + 2) + half < nkt) gload((2 * (pi + 2) + half) * KT);
         }
         __syncthreads();
     }
 
-    // both halves of the wave hold partial sums for the same query: combine
-    // them with every lane active
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float t_tot = t_run + __shfl_xor(t_run, 32, 64);
+    // Merge the two key halves through LDS (the stage buffers are free now).
+    float* xch = reinterpret_cast<float*>(smem);
+    constexpr int XW = DT * 4 + 3;  // floats per lane: O, m, l, t
+    if (half == 1) {
+        float* dst = xch + (rw * 64 + lane) * XW;
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[d * 4 + j] = oacc[d][j];
+        dst[DT * 4] = m_ref;
+        dst[DT * 4 + 1] = lacc[0];
+        dst[DT * 4 + 2] = t_part;
+    }
+    __syncthreads();
+    if (half == 1) return;
+    {
+        const float* src = xch + (rw * 64 + lane) * XW;
+        const float m2 = src[DT * 4];
+        const float m_new = fmaxf(m_ref, m2);
+        const float a1 = (m_ref == -INFINITY) ? 0.0f : fast_exp2(m_ref - m_new);
+        const float a2 = (m2 == -INFINITY) ? 0.0f : fast_exp2(m2 - m_new);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) oacc[d][j] = oacc[d][j] * a1 + src[d * 4 + j] * a2;
+        lacc[0] = lacc[0] * a1 + src[DT * 4 + 1] * a2;
+        t_part = t_part * a1 + src[DT * 4 + 2] * a2;
+        m_ref = m_new;
+    }
+
+    // lacc already sums over all keys of the row; t is per lane group
+    const float l_tot = lacc[0];
+    float t_tot = t_part + __shfl_xor(t_part, 16, 64);
+    t_tot += __shfl_xor(t_tot, 32, 64);
     const float inv_l = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (!row_ok) return;
     const int h = myrow % H;
     if constexpr (MODE == 0) {
         f16* Ob = p.out + (int64_t)b * NH * DH + (int64_t)myrow * DH;
 #pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4) {
-                const int dh = t * 32 + 8 * e4 + 4 * lg;
-                u32x2 w = {pack_h2(oacc[t][4 * e4] * inv_l, oacc[t][4 * e4 + 1] * inv_l),
-                           pack_h2(oacc[t][4 * e4 + 2] * inv_l, oacc[t][4 * e4 + 3] * inv_l)};
-                *reinterpret_cast<u32x2*>(Ob + dh) = w;
-            }
-        if (p.lse && lg == 0) {
-            float lse = (l_tot > 0.0f) ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+        for (int d = 0; d < DT; ++d) {
+            u32x2 w = {pack_h2(oacc[d][0] * inv_l, oacc[d][1] * inv_l),
+                       pack_h2(oacc[d][2] * inv_l, oacc[d][3] * inv_l)};
+            *reinterpret_cast<u32x2*>(Ob + d * 16 + g * 4) = w;
+        }
+        if (p.lse && g == 0) {
+            const float lse = (l_tot > 0.0f) ? (m_ref + log2f(l_tot)) * kLn2 : -INFINITY;
             p.lse[((int64_t)b * H + h) * N + qpos] = lse;
         }
     } else {
-        if (lg == 0) {
-            p.lse2_rows[(int64_t)b * NH + myrow] = (l_tot > 0.0f) ? m_run + log2f(l_tot) : INFINITY;
+        if (g == 0) {
+            p.lse2_rows[(int64_t)b * NH + myrow] = (l_tot > 0.0f) ? m_ref + log2f(l_tot) : INFINITY;
             p.d_rows[(int64_t)b * NH + myrow] = t_tot * inv_l;
         }
     }
@@ -700,13 +833,17 @@ size_t g_bwd_ws_elems = 0;
 
 template <int DH>
 hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st) {
-    dim3 grid((a.N * a.H + BR - 1) / BR, a.B);
+    const int nrg = (a.N * a.H + FR - 1) / FR;
+    dim3 grid(nrg * a.B);
+    // zigzag round = one workgroup per CU: round r+1 runs in reverse, so the
+    // workgroups that land on the same CU pair heavy with light row groups
+    const int round = device_cu_count();
     if (mode == 0) {
-        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 0>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((flash_fwd<DH, false, 0>), grid, dim3(256), 0, st, a);
+        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 0>), grid, dim3(512), 0, st, a, round);
+        else hipLaunchKernelGGL((flash_fwd<DH, false, 0>), grid, dim3(512), 0, st, a, round);
     } else {
-        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 1>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((flash_fwd<DH, false, 1>), grid, dim3(256), 0, st, a);
+        if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 1>), grid, dim3(512), 0, st, a, round);
+        else hipLaunchKernelGGL((flash_fwd<DH, false, 1>), grid, dim3(512), 0, st, a, round);
     }
     return hipGetLastError();
 }
