@@ -72,6 +72,14 @@ def build(verbose: bool = False) -> None:
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + api +
              ["-L", HERE, "-levkhip", "-Wl,-rpath,$ORIGIN"])
         os.replace(tmp, lib)
+    if api:
+        # the evk / evk::ai API tests (tests/cpp), linked against libevk.so
+        os.makedirs(os.path.join(HERE, "bin"), exist_ok=True)
+        exe = os.path.join(HERE, "bin", "api_tests")
+        _run([HIPCC, "-x", "hip", "--offload-arch=" + ARCH] + HIP_FLAGS[1:] +
+             [os.path.join(ROOT, "tests", "cpp", "api_tests.cpp"), "-o", exe + ".tmp",
+              "-L", HERE, "-levk", "-levkhip", "-Wl,-rpath,$ORIGIN/.."])
+        os.replace(exe + ".tmp", exe)
     if verbose:
         print("built", kern)
 

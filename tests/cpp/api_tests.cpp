@@ -1,0 +1,629 @@
+// Tests of the evk / evk::ai C++ API (include/evk.h, include/evk_ai.h) on
+// the gfx950 kernels, written against the API the way the reference's
+// example/tests.h is: each test prints TEST(...) [PASS]/[FAIL] and the
+// program exits non-zero at the first failure.
+//
+//   api_tests            every test (needs the GPU)
+//   api_tests --cpu      host-only tests: float16_t conversions, Shape
+//
+// Known answers follow example/tests.h: add :139-161, matmul identity
+// :163-194, broadcast :196-219, flash backward head sum :401-471, flash vs
+// unfused softmax attention :473-563, gelu :1169-1190, embed :1224-1252,
+// rope :1318-1356, rms_norm :1411-1444, greedy :1472-1497, flash backward
+// with Q=K=V=0 :1499-1563.
+#include <evk_ai.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#define TEST(expr)                                                            \
+    do {                                                                      \
+        if (expr) {                                                           \
+            std::printf(" TEST(" #expr ") [PASS]\n");                        \
+        } else {                                                              \
+            std::printf(" TEST(" #expr ") [FAIL] [%s:%d]\n", __FILE__, __LINE__); \
+            std::fflush(stdout);                                              \
+            std::exit(1);                                                     \
+        }                                                                     \
+    } while (0)
+
+static bool near(float a, float b, float tol) {
+    return std::fabs(a - b) <= tol;
+}
+
+static float gelu_ref(float x) {
+    return 0.5f * x * (1.0f + std::tanh(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+}
+
+// deterministic inputs: a small LCG (the reference uses platform rand())
+struct Lcg {
+    uint64_t s;
+    explicit Lcg(uint64_t seed) : s(seed * 2862933555777941757ull + 3037000493ull) {}
+    float uniform() {  // [-1, 1)
+        s = s * 6364136223846793005ull + 1442695040888963407ull;
+        return float(int64_t(s >> 40) - (1ll << 23)) / float(1 << 23);
+    }
+};
+
+static void upload(Tensor& t, const std::vector<float>& v) {
+    float16_t* h = t.cpu();
+    for (size_t i = 0; i < v.size(); ++i) h[i] = float16_t(v[i]);
+    t.cpu_upload();
+}
+static std::vector<float> download(Tensor& t) {
+    t.cpu_download();
+    const float16_t* h = t.cpu();
+    return std::vector<float>(h, h + t.shape.count());
+}
+static std::vector<float> random_vec(size_t n, uint64_t seed, float scale = 1.0f) {
+    Lcg g(seed);
+    std::vector<float> v(n);
+    for (float& x : v) x = float(float16_t(scale * g.uniform()));  // fp16-representable
+    return v;
+}
+
+// ------------------------------------------------------------------ host only
+static void test_float16_conversions() {
+    std::printf("test_float16_conversions()\n");
+    TEST(float16_t(1.0f).value == 0x3C00u);
+    TEST(float16_t(-2.0f).value == 0xC000u);
+    TEST(float16_t(65504.0f).value == 0x7BFFu);
+    TEST(float16_t(65520.0f).value == 0x7C00u);                    // rounds up to inf
+    TEST(float16_t(1.0f + 1.0f / 2048.0f).value == 0x3C00u);       // tie -> even
+    TEST(float16_t(1.0f + 3.0f / 2048.0f).value == 0x3C02u);       // tie -> even (up)
+    TEST(float16_t(std::ldexp(1.0f, -24)).value == 0x0001u);       // smallest subnormal
+    TEST(float16_t(std::ldexp(1.0f, -25)).value == 0x0000u);       // below 2^-24 flushes
+    TEST(float16_t(std::ldexp(3.0f, -26)).value == 0x0000u);       // 0.75 ulp flushes (IEEE: 1)
+    TEST(float16_t(std::ldexp(5.0f, -25)).value == 0x0003u);       // 2.5 ulp rounds half-up (IEEE: 2)
+    TEST(float16_t(std::ldexp(9.0f, -26)).value == 0x0002u);       // 2.25 ulp rounds down
+    TEST(float16_t(INFINITY).value == 0x7C00u);
+    TEST((float16_t(NAN).value & 0x7C00u) == 0x7C00u && (float16_t(NAN).value & 0x3FFu) != 0);
+    bool exact = true;
+    for (uint32_t h = 0; h < 0x7C00u; ++h) {  // every finite positive half round-trips
+        float16_t x;
+        x.value = uint16_t(h);
+        if (float16_t(float(x)).value != h) exact = false;
+    }
+    TEST(exact);
+    float16_t a(1.5f);
+    a += float16_t(2.0f);
+    TEST(float(a) == 3.5f);
+    a /= float16_t(2.0f);
+    TEST(float(a) == 1.75f);
+}
+
+static void test_shape() {
+    std::printf("test_shape()\n");
+    Shape s({2, 3, 4, 5});
+    TEST(s.rank() == 4 && s.count() == 120);
+    TEST(s[-1] == 5 && s[-2] == 4 && s[0] == 2);
+    TEST(s.batch_size(2) == 6 && s.batch_size(0) == 120 && s.batch_size(4) == 1);
+    TEST(s.number_of_elements(1) == 60);
+    Shape e;
+    TEST(e.rank() == 0 && e.count() == 1);
+}
+
+// ------------------------------------------------------------------ runtime
+static void test_runtime_commands() {
+    std::printf("test_runtime_commands()\n");
+    TEST(evk::GetFeatures().coopmat);
+    evk::Buffer gpu = evk::CreateBuffer({.size = 4096, .usage = evk::BufferUsage::Storage});
+    evk::Buffer host = evk::CreateBuffer({.size = 4096, .usage = evk::BufferUsage::TransferDst,
+                                          .memoryType = evk::MemoryType::GPU_TO_CPU});
+    TEST(gpu.GetPtr() == nullptr && gpu.GetReference() != 0);
+    TEST(host.GetPtr() != nullptr && host.GetSize() == 4096);
+    std::vector<uint32_t> src(1024);
+    for (uint32_t i = 0; i < 1024; ++i) src[i] = i * 2654435761u;
+    evk::Cmd& cmd = evk::CmdBegin();
+    cmd.fill(gpu, 0xDEADBEEFu, 4096);
+    cmd.copy(src.data(), gpu, 2048, 1024);  // staged: src may change right after
+    std::fill(src.begin(), src.end(), 0u);
+    cmd.barrier();
+    cmd.copy(gpu, host, 4096);
+    const uint64_t idx = cmd.submit();
+    evk::CmdWait(idx);
+    TEST(evk::CmdDone(idx));
+    const uint32_t* h = static_cast<const uint32_t*>(host.GetPtr());
+    bool ok = true;
+    for (uint32_t i = 0; i < 1024; ++i) {
+        const uint32_t want = (i >= 256 && i < 768) ? (i - 256) * 2654435761u : 0xDEADBEEFu;
+        if (h[i] != want) ok = false;
+    }
+    TEST(ok);
+    std::vector<uint8_t> back(4096);
+    evk::ReadBuffer(gpu, back.data(), 4096);
+    TEST(std::memcmp(back.data(), host.GetPtr(), 4096) == 0);
+    // buffers released while work is queued are freed after it (no stall, no fault)
+    for (int i = 0; i < 64; ++i) {
+        Tensor t({1024, 1024});
+        evk::ai::zero(t);
+    }
+    evk::ai::SubmitCmd(true);
+    TEST(evk::GetMemoryBudget().heaps[0].budget > (64ull << 30));
+}
+
+// ------------------------------------------------------------------ ops
+static void test_add() {
+    std::printf("test_add()\n");
+    Tensor a({4}), b({4}), out({4});
+    upload(a, {0, 1, 2, 3});
+    upload(b, {0, 2, 4, 6});
+    evk::ai::add(a, b, out);
+    std::vector<float> o = download(out);
+    for (uint32_t i = 0; i < 4; ++i) TEST(o[i] == float(3 * i));
+}
+
+static void test_matmul() {
+    std::printf("test_matmul()\n");
+    const uint32_t n = 400;
+    Tensor a({n, n}), b({n, n}), c({n, n});
+    a.identity(2.0f);
+    b.identity(2.0f);
+    evk::ai::matmul(a, b, c);
+    c.cpu_download();
+    bool diag = true, off = true;
+    for (uint32_t i = 0; i < n * n; ++i) {
+        const float v = float(c.cpu()[i]);
+        if (i / n == i % n) {
+            diag &= (v == 4.0f);
+        } else {
+            off &= (v == 0.0f);
+        }
+    }
+    TEST(diag);
+    TEST(off);
+}
+
+static void test_matmul_broadcast() {
+    std::printf("test_matmul_broadcast()\n");
+    Tensor a({1, 32, 32}), b({32, 32}), c({3, 32, 32});
+    a.fill(float16_t(1.0f));
+    b.identity(float16_t(1.0f));
+    evk::ai::matmul(a, b, c, false, false, false, 16, 16);
+    std::vector<float> o = download(c);
+    bool ok = true;
+    for (float v : o) ok &= (v == 1.0f);
+    TEST(ok);
+}
+
+// C = op(A) op(B) (+ C) against an fp64 host loop, every transpose combination.
+static void test_matmul_vs_cpu() {
+    std::printf("test_matmul_vs_cpu()\n");
+    const uint32_t M = 96, N = 80, K = 112;
+    for (int mode = 0; mode < 5; ++mode) {
+        const bool ta = mode & 1, tb = mode & 2, acc = mode == 4;
+        std::vector<float> A = random_vec(size_t(M) * K, 11 + mode), B = random_vec(size_t(K) * N, 21 + mode);
+        std::vector<float> C0 = random_vec(size_t(M) * N, 31 + mode);
+        Tensor a(ta ? Shape({K, M}) : Shape({M, K})), b(tb ? Shape({N, K}) : Shape({K, N})), c({M, N});
+        upload(a, A);
+        upload(b, B);
+        upload(c, C0);
+        evk::ai::matmul(a, b, c, ta, tb, acc);
+        std::vector<float> got = download(c);
+        float worst = 0.0f;
+        for (uint32_t i = 0; i < M; ++i) {
+            for (uint32_t j = 0; j < N; ++j) {
+                double s = acc ? C0[size_t(i) * N + j] : 0.0;
+                for (uint32_t k = 0; k < K; ++k) {
+                    const float x = ta ? A[size_t(k) * M + i] : A[size_t(i) * K + k];
+                    const float y = tb ? B[size_t(j) * K + k] : B[size_t(k) * N + j];
+                    s += double(x) * y;
+                }
+                worst = std::max(worst, float(std::fabs(got[size_t(i) * N + j] - s) / (1.0 + std::fabs(s))));
+            }
+        }
+        std::printf("  mode ta=%d tb=%d acc=%d  max rel err %.2e\n", ta, tb, acc, worst);
+        TEST(worst <= 1e-2f);
+    }
+}
+
+// Host attention in fp64 (MQA, optional causal), returns O and the row LSE.
+static void cpu_attention(const std::vector<float>& q, const std::vector<float>& k, const std::vector<float>& v,
+                          uint32_t B, uint32_t N, uint32_t H, uint32_t Dh, bool causal, std::vector<float>& o,
+                          std::vector<float>& lse) {
+    const uint32_t D = H * Dh;
+    o.assign(size_t(B) * N * D, 0.0f);
+    lse.assign(size_t(B) * H * N, 0.0f);
+    std::vector<double> s(N);
+    const double scale = 1.0 / std::sqrt(double(Dh));
+    for (uint32_t b = 0; b < B; ++b)
+        for (uint32_t h = 0; h < H; ++h)
+            for (uint32_t i = 0; i < N; ++i) {
+                const uint32_t L = causal ? i + 1 : N;
+                double m = -1e300;
+                for (uint32_t j = 0; j < L; ++j) {
+                    double d = 0;
+                    for (uint32_t x = 0; x < Dh; ++x)
+                        d += double(q[(size_t(b) * N + i) * D + h * Dh + x]) * k[(size_t(b) * N + j) * Dh + x];
+                    s[j] = d * scale;
+                    m = std::max(m, s[j]);
+                }
+                double l = 0;
+                for (uint32_t j = 0; j < L; ++j) l += (s[j] = std::exp(s[j] - m));
+                for (uint32_t x = 0; x < Dh; ++x) {
+                    double acc = 0;
+                    for (uint32_t j = 0; j < L; ++j) acc += s[j] * v[(size_t(b) * N + j) * Dh + x];
+                    o[(size_t(b) * N + i) * D + h * Dh + x] = float(acc / l);
+                }
+                lse[(size_t(b) * H + h) * N + i] = float(m + std::log(l));
+            }
+}
+
+static void test_flash_attention_vs_cpu() {
+    std::printf("test_flash_attention_vs_cpu()\n");
+    const uint32_t B = 2, N = 192, H = 4, Dh = 64, D = H * Dh;
+    for (int causal = 0; causal < 2; ++causal) {
+        std::vector<float> q = random_vec(size_t(B) * N * D, 41, 2.0f), k = random_vec(size_t(B) * N * Dh, 42, 2.0f),
+                           v = random_vec(size_t(B) * N * Dh, 43);
+        Tensor tq({B, N, D}), tk({B, N, Dh}), tv({B, N, Dh}), to({B, N, D}), tl({B, H, N, 2});
+        upload(tq, q);
+        upload(tk, k);
+        upload(tv, v);
+        evk::ai::flash_attention(tq, tk, tv, to, causal, &tl);
+        std::vector<float> o = download(to), wo, wl;
+        tl.cpu_download();
+        const float* lse = reinterpret_cast<const float*>(tl.cpu());
+        cpu_attention(q, k, v, B, N, H, Dh, causal, wo, wl);
+        float eo = 0, el = 0;
+        for (size_t i = 0; i < o.size(); ++i) eo = std::max(eo, std::fabs(o[i] - wo[i]) / (1.0f + std::fabs(wo[i])));
+        for (size_t i = 0; i < wl.size(); ++i) el = std::max(el, std::fabs(lse[i] - wl[i]));
+        std::printf("  causal=%d  O max rel err %.2e  LSE max abs err %.2e\n", causal, eo, el);
+        TEST(eo <= 1e-2f);
+        TEST(el <= 1e-3f);
+    }
+}
+
+// Flash forward against the unfused path (two GEMMs with softmax between),
+// the reference's own GPU-side cross-check; the softmax runs on the host
+// since this library has no standalone softmax op.
+static void test_flash_attention_cmp_softmax() {
+    std::printf("test_flash_attention_cmp_softmax()\n");
+    const uint32_t N = 2048, Dh = 64;
+    Tensor q({1, N, Dh}), k({1, N, Dh}), v({1, N, Dh}), of({1, N, Dh});
+    Tensor qs({1, N, Dh}), s({1, N, N}), p({1, N, N}), ob({1, N, Dh});
+    std::vector<float> Q(size_t(N) * Dh), K(size_t(N) * Dh), V(size_t(N) * Dh), QS(size_t(N) * Dh);
+    for (uint32_t i = 0; i < N; ++i)
+        for (uint32_t d = 0; d < Dh; ++d) {
+            Q[size_t(i) * Dh + d] = float((i + d) % 13) / 13.0f;
+            K[size_t(i) * Dh + d] = float((i * 7 + d) % 11) / 11.0f;
+            V[size_t(i) * Dh + d] = float((i + 3 * d) % 17) / 17.0f;
+        }
+    for (size_t i = 0; i < QS.size(); ++i) QS[i] = float(float16_t(float(float16_t(Q[i])) * 0.125f));
+    upload(q, Q);
+    upload(k, K);
+    upload(v, V);
+    upload(qs, QS);
+    evk::ai::flash_attention(q, k, v, of);
+    evk::ai::matmul(qs, k, s, false, true, false, 64, 64);
+    std::vector<float> S = download(s);
+    float16_t* P = p.cpu();
+    for (uint32_t i = 0; i < N; ++i) {
+        float m = -FLT_MAX;
+        for (uint32_t j = 0; j < N; ++j) m = std::max(m, S[size_t(i) * N + j]);
+        double l = 0;
+        for (uint32_t j = 0; j < N; ++j) l += std::exp(double(S[size_t(i) * N + j] - m));
+        for (uint32_t j = 0; j < N; ++j) P[size_t(i) * N + j] = float16_t(float(std::exp(double(S[size_t(i) * N + j] - m)) / l));
+    }
+    p.cpu_upload();
+    evk::ai::matmul(p, v, ob, false, false, false, 64, 64);
+    std::vector<float> a = download(of), b = download(ob);
+    float worst = 0;
+    for (size_t i = 0; i < a.size(); ++i) worst = std::max(worst, std::fabs(a[i] - b[i]));
+    std::printf("  max |flash - unfused| = %.3e\n", worst);
+    TEST(worst <= 5e-2f);
+}
+
+static void test_flash_attention_backward() {
+    std::printf("test_flash_attention_backward()\n");
+    const uint32_t B = 1, N = 16, Dh = 16, H = 2, D = H * Dh;
+    Tensor q({B, N, D}), k({B, N, Dh}), v({B, N, Dh}), o({B, N, D}), dO({B, N, D});
+    Tensor dQ({B, N, D}), dK({B, N, Dh}), dV({B, N, Dh});
+    q.fill(float16_t(0.0f));
+    k.fill(float16_t(0.0f));
+    v.fill(float16_t(0.0f));
+    std::vector<float> g(size_t(N) * D, 0.0f);
+    for (uint32_t d = 0; d < D; ++d) g[d] = float(d + 1);  // only row 0 of dO
+    upload(dO, g);
+    evk::ai::flash_attention_bwd(q, k, v, o, dO, dQ, dK, dV);
+    std::vector<float> gq = download(dQ), gk = download(dK), gv = download(dV);
+    bool okq = true, okk = true, okv = true;
+    for (float x : gq) okq &= std::fabs(x) <= 1e-2f;
+    for (float x : gk) okk &= std::fabs(x) <= 1e-2f;
+    for (uint32_t j = 0; j < N; ++j)
+        for (uint32_t x = 0; x < Dh; ++x) {
+            float mean = 0;
+            for (uint32_t h = 0; h < H; ++h) mean += g[h * Dh + x];
+            okv &= near(gv[size_t(j) * Dh + x], mean / N, 5e-2f);
+        }
+    TEST(okq);
+    TEST(okk);
+    TEST(okv);
+}
+
+static void test_flash_attention_backward_scratch() {
+    std::printf("test_flash_attention_backward_scratch()\n");
+    const uint32_t N = 16, Dh = 32;
+    Tensor q({1, N, Dh}), k({1, N, Dh}), v({1, N, Dh}), o({1, N, Dh}), dO({1, N, Dh});
+    Tensor dQ({1, N, Dh}), dK({1, N, Dh}), dV({1, N, Dh});
+    q.fill(float16_t(0.0f));
+    k.fill(float16_t(0.0f));
+    v.fill(float16_t(0.0f));
+    std::vector<float> g(size_t(N) * Dh);
+    for (uint32_t i = 0; i < N; ++i)
+        for (uint32_t d = 0; d < Dh; ++d) g[size_t(i) * Dh + d] = float(d + 1);
+    upload(dO, g);
+    evk::ai::flash_attention_bwd(q, k, v, o, dO, dQ, dK, dV);
+    std::vector<float> gq = download(dQ), gk = download(dK), gv = download(dV);
+    bool okq = true, okk = true, okv = true;
+    for (float x : gq) okq &= x == 0.0f;
+    for (float x : gk) okk &= x == 0.0f;
+    for (uint32_t j = 0; j < N; ++j)
+        for (uint32_t d = 0; d < Dh; ++d) okv &= near(gv[size_t(j) * Dh + d], float(d + 1), 8e-2f);
+    TEST(okq);
+    TEST(okk);
+    TEST(okv);
+}
+
+// Causal backward through the saved LSE against finite differences of the
+// host forward: a scalar loss <dO, O> perturbed along one coordinate.
+static void test_flash_attention_backward_with_lse() {
+    std::printf("test_flash_attention_backward_with_lse()\n");
+    const uint32_t B = 1, N = 64, H = 2, Dh = 32, D = H * Dh;
+    std::vector<float> Q = random_vec(size_t(N) * D, 51), K = random_vec(size_t(N) * Dh, 52),
+                       V = random_vec(size_t(N) * Dh, 53), G = random_vec(size_t(N) * D, 54);
+    Tensor q({B, N, D}), k({B, N, Dh}), v({B, N, Dh}), o({B, N, D}), dO({B, N, D}), lse({B, H, N, 2});
+    Tensor dQ({B, N, D}), dK({B, N, Dh}), dV({B, N, Dh});
+    upload(q, Q);
+    upload(k, K);
+    upload(v, V);
+    upload(dO, G);
+    evk::ai::flash_attention(q, k, v, o, true, &lse);
+    evk::ai::flash_attention_bwd(q, k, v, o, dO, dQ, dK, dV, H, true, &lse);
+    std::vector<float> gq = download(dQ), gk = download(dK), gv = download(dV);
+    auto loss = [&](const std::vector<float>& q_, const std::vector<float>& k_, const std::vector<float>& v_) {
+        std::vector<float> oo, ll;
+        cpu_attention(q_, k_, v_, B, N, H, Dh, true, oo, ll);
+        double s = 0;
+        for (size_t i = 0; i < oo.size(); ++i) s += double(oo[i]) * G[i];
+        return s;
+    };
+    const double hstep = 1e-2;
+    float worst = 0;
+    const size_t probes[3] = {5, 1000, 2047};
+    for (int which = 0; which < 3; ++which) {
+        for (size_t idx : probes) {
+            std::vector<float> q2 = Q, k2 = K, v2 = V;
+            std::vector<float>& t = which == 0 ? q2 : which == 1 ? k2 : v2;
+            const size_t i = idx % t.size();
+            const float x0 = t[i];
+            t[i] = float(x0 + hstep);
+            const double up = loss(q2, k2, v2);
+            t[i] = float(x0 - hstep);
+            const double dn = loss(q2, k2, v2);
+            const double fd = (up - dn) / (2 * hstep);
+            const float got = (which == 0 ? gq : which == 1 ? gk : gv)[i];
+            worst = std::max(worst, float(std::fabs(got - fd) / (1.0 + std::fabs(fd))));
+        }
+    }
+    std::printf("  max rel err vs finite differences %.2e\n", worst);
+    TEST(worst <= 2e-2f);
+}
+
+static void test_single_query_attention() {
+    std::printf("test_single_query_attention()\n");
+    const uint32_t H = 12, dh = 64, d = H * dh, L = 300, maxL = 320;
+    std::vector<float> q = random_vec(d, 61, 2.0f), kc = random_vec(size_t(maxL) * d, 62, 2.0f),
+                       vc = random_vec(size_t(maxL) * d, 63);
+    Tensor tq({d}), tk({maxL, d}), tv({maxL, d}), out({d});
+    upload(tq, q);
+    upload(tk, kc);
+    upload(tv, vc);
+    evk::ai::single_query_attention(tq, tk, tv, out, L, H);
+    std::vector<float> got = download(out);
+    float worst = 0;
+    for (uint32_t h = 0; h < H; ++h) {
+        std::vector<double> s(L);
+        double m = -1e300;
+        for (uint32_t j = 0; j < L; ++j) {
+            double x = 0;
+            for (uint32_t e = 0; e < dh; ++e) x += double(q[h * dh + e]) * kc[size_t(j) * d + h * dh + e];
+            s[j] = x / 8.0;
+            m = std::max(m, s[j]);
+        }
+        double l = 0;
+        for (double& x : s) l += (x = std::exp(x - m));
+        for (uint32_t e = 0; e < dh; ++e) {
+            double acc = 0;
+            for (uint32_t j = 0; j < L; ++j) acc += s[j] * vc[size_t(j) * d + h * dh + e];
+            worst = std::max(worst, float(std::fabs(got[h * dh + e] - acc / l)));
+        }
+    }
+    std::printf("  max abs err %.2e\n", worst);
+    TEST(worst <= 1e-2f);
+    // L = 1 attends to row 0 only: out == V[0]
+    evk::ai::single_query_attention(tq, tk, tv, out, 1, H);
+    got = download(out);
+    bool ok = true;
+    for (uint32_t e = 0; e < d; ++e) ok &= got[e] == vc[e];
+    TEST(ok);
+}
+
+static void test_gelu() {
+    std::printf("test_gelu()\n");
+    Tensor in({3}), out({3});
+    const float xs[3] = {-1.0f, 0.0f, 1.0f};
+    upload(in, {xs[0], xs[1], xs[2]});
+    evk::ai::gelu(in, out);
+    std::vector<float> o = download(out);
+    for (int i = 0; i < 3; ++i) TEST(near(o[i], gelu_ref(xs[i]), 2e-2f));
+}
+
+static void test_embed() {
+    std::printf("test_embed()\n");
+    Tensor table({4, 3}), ids({2}), out({2, 3});
+    std::vector<float> t(12);
+    for (int i = 0; i < 12; ++i) t[i] = float(i + 1);
+    upload(table, t);
+    float16_t* ip = ids.cpu();
+    ip[0].value = 1;
+    ip[1].value = 3;
+    ids.cpu_upload();
+    evk::ai::embed(table, ids, out);
+    std::vector<float> o = download(out);
+    for (int e = 0; e < 3; ++e) {
+        TEST(o[e] == t[3 + e]);
+        TEST(o[3 + e] == t[9 + e]);
+    }
+}
+
+static void test_rope() {
+    std::printf("test_rope()\n");
+    const uint32_t N = 2, D = 4;
+    const float x[8] = {1, 2, 3, 4, 5, 6, 7, 8};
+    Tensor in({1, N, D}), out({1, N, D});
+    upload(in, std::vector<float>(x, x + 8));
+    evk::ai::rope(in, out, 1, N, D, 10000.0f);
+    std::vector<float> o = download(out);
+    for (uint32_t t = 0; t < N; ++t)
+        for (uint32_t p = 0; p < D / 2; ++p) {
+            const float th = float(t) * std::pow(10000.0f, -2.0f * float(p) / float(D));
+            const float c = std::cos(th), s = std::sin(th), x0 = x[t * D + 2 * p], x1 = x[t * D + 2 * p + 1];
+            TEST(near(o[t * D + 2 * p], x0 * c - x1 * s, 3e-2f));
+            TEST(near(o[t * D + 2 * p + 1], x0 * s + x1 * c, 3e-2f));
+        }
+    // per-head rotation at an absolute position equals the plain rope of that row
+    const uint32_t H = 3, hd = 8, pos = 37;
+    std::vector<float> v = random_vec(H * hd, 71);
+    Tensor one({1, 1, H * hd}), rot({1, 1, H * hd});
+    upload(one, v);
+    evk::ai::rope(one, rot, 1, 1, H * hd, 10000.0f, pos, hd);
+    std::vector<float> r = download(rot);
+    bool ok = true;
+    for (uint32_t h = 0; h < H; ++h) {
+        Tensor seq({1, pos + 1, hd}), seq_out({1, pos + 1, hd});
+        std::vector<float> s(size_t(pos + 1) * hd, 0.0f);
+        for (uint32_t e = 0; e < hd; ++e) s[size_t(pos) * hd + e] = v[h * hd + e];
+        upload(seq, s);
+        evk::ai::rope(seq, seq_out, 1, pos + 1, hd, 10000.0f);
+        std::vector<float> so = download(seq_out);
+        for (uint32_t e = 0; e < hd; ++e) ok &= so[size_t(pos) * hd + e] == r[h * hd + e];
+    }
+    TEST(ok);
+}
+
+static void test_rms_norm() {
+    std::printf("test_rms_norm()\n");
+    const float x[8] = {3, 4, 0, 0, 1, 2, 3, 4};
+    Tensor in({2, 4}), out({2, 4});
+    upload(in, std::vector<float>(x, x + 8));
+    evk::ai::rms_norm(in, out, 1e-4f);
+    std::vector<float> o = download(out);
+    for (int r = 0; r < 2; ++r) {
+        float ss = 0;
+        for (int d = 0; d < 4; ++d) ss += x[r * 4 + d] * x[r * 4 + d];
+        const float inv = 1.0f / std::sqrt(ss / 4.0f + 1e-4f);
+        for (int d = 0; d < 4; ++d) TEST(near(o[r * 4 + d], x[r * 4 + d] * inv, 3e-2f));
+    }
+}
+
+static void test_greedy_sample() {
+    std::printf("test_greedy_sample()\n");
+    Tensor logits({2, 2, 5}), tok({2});
+    std::vector<float> l(20, -10.0f);
+    l[(0 * 2 + 1) * 5 + 1] = 0.5f;
+    l[(0 * 2 + 1) * 5 + 2] = 2.5f;
+    l[(0 * 2 + 1) * 5 + 3] = 1.5f;
+    l[(1 * 2 + 1) * 5 + 1] = 3.0f;
+    l[(1 * 2 + 1) * 5 + 2] = 2.0f;
+    l[(1 * 2 + 1) * 5 + 3] = 1.0f;
+    upload(logits, l);
+    evk::ai::greedy_sample(logits, tok, 1, 1, 3);
+    tok.cpu_download();
+    TEST(tok.cpu()[0].value == 2u);
+    TEST(tok.cpu()[1].value == 1u);
+}
+
+static void test_timestamps() {
+    std::printf("test_timestamps()\n");
+    const uint32_t n = 1024;
+    Tensor a({n, n}), b({n, n}), c({n, n});
+    a.fill(float16_t(0.5f));
+    b.fill(float16_t(0.25f));
+    evk::Cmd& cmd = evk::ai::GetCmd();
+    for (int i = 0; i < 4; ++i) cmd.timestamp("matmul", [&]() { evk::ai::matmul(a, b, c); });
+    evk::ai::SubmitCmd(true);
+    const auto& ts = evk::CmdTimestamps();
+    TEST(ts.size() == 4);
+    bool ordered = true;
+    for (const auto& t : ts) ordered &= (t.end >= t.start) && std::strcmp(t.name, "matmul") == 0;
+    TEST(ordered);
+    std::printf("  matmul 1024^3: %.3f ms\n", ts.empty() ? 0.0 : ts.back().end - ts.back().start);
+    std::vector<float> o = download(c);
+    bool exact = true;
+    for (float x : o) exact &= x == 128.0f;  // 1024 * 0.5 * 0.25, exact in fp32
+    TEST(exact);
+    Tensor one({1});
+    one.fill(float16_t(3.0f));
+    TEST(float(one.item()) == 3.0f);
+}
+
+// Writes float16_t(x).value for the fp32 bit patterns i * 4093 (i < 2^20),
+// which spread over every exponent and sign, as raw uint16 to `path`.
+static int f16_sweep(const char* path) {
+    std::FILE* f = std::fopen(path, "wb");
+    if (!f) return 1;
+    std::vector<uint16_t> out(1u << 20);
+    for (uint32_t i = 0; i < (1u << 20); ++i) {
+        const uint32_t bits = i * 4093u;
+        float x;
+        std::memcpy(&x, &bits, 4);
+        out[i] = float16_t(x).value;
+    }
+    const size_t n = std::fwrite(out.data(), 2, out.size(), f);
+    std::fclose(f);
+    return n == out.size() ? 0 : 1;
+}
+
+int main(int argc, char** argv) {
+    std::setvbuf(stdout, nullptr, _IONBF, 0);  // a crash still shows the last test
+    if (argc > 2 && std::strcmp(argv[1], "--f16-sweep") == 0) return f16_sweep(argv[2]);
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    test_float16_conversions();
+    test_shape();
+    if (cpu_only) {
+        std::printf("ALL PASSED (host)\n");
+        return 0;
+    }
+    evk::EvkDesc desc;
+    desc.applicationName = "evk api tests";
+    desc.enableTimestamps = true;
+    if (!evk::InitializeEVK(desc)) {
+        std::printf("no gfx950 device\n");
+        return 2;
+    }
+    evk::ai::initialize();
+    test_runtime_commands();
+    test_add();
+    test_matmul();
+    test_matmul_broadcast();
+    test_matmul_vs_cpu();
+    test_flash_attention_vs_cpu();
+    test_flash_attention_cmp_softmax();
+    test_flash_attention_backward();
+    test_flash_attention_backward_scratch();
+    test_flash_attention_backward_with_lse();
+    test_single_query_attention();
+    test_gelu();
+    test_embed();
+    test_rope();
+    test_rms_norm();
+    test_greedy_sample();
+    test_timestamps();
+    evk::ai::shutdown();
+    std::printf("ALL PASSED\n");
+    return 0;
+}

@@ -1,0 +1,117 @@
+// Recording stand-in for the evkhip C ABI; see evkhip_stub.h.
+#include "evkhip_stub.h"
+
+#include <evk_ai.h>  // float16_t
+
+#include <cstring>
+
+namespace {
+StubCall g_last;
+int g_count = 0;
+int g_fail_status = 0;
+std::string g_fail_msg, g_error;
+
+uint64_t elems(const evkhip_tensor* t) {
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < t->rank; ++i) n *= t->dims[i];
+    return n;
+}
+
+int record(const char* name, std::initializer_list<const evkhip_tensor*> ts, std::initializer_list<long long> ints,
+           std::initializer_list<double> floats, void* stream, const void* ptr = nullptr) {
+    ++g_count;
+    g_last = StubCall{};
+    g_last.name = name;
+    for (const evkhip_tensor* t : ts) {
+        g_last.tensors.push_back(*t);
+        if (t->data && !mock_stream_access(t->data, elems(t) * 2)) return EVKHIP_ERR_INVALID_ARG;
+    }
+    g_last.ints = ints;
+    g_last.floats = floats;
+    g_last.stream = stream;
+    g_last.ptr = ptr;
+    if (g_fail_status) {
+        const int s = g_fail_status;
+        g_fail_status = 0;
+        g_error = g_fail_msg;
+        return s;
+    }
+    return EVKHIP_OK;
+}
+}  // namespace
+
+const StubCall& stub_last_call() {
+    return g_last;
+}
+int stub_call_count() {
+    return g_count;
+}
+void stub_fail_next(int status, const char* msg) {
+    g_fail_status = status;
+    g_fail_msg = msg;
+}
+
+extern "C" {
+
+const char* evkhip_version(void) {
+    return "evkhip stub";
+}
+const char* evkhip_last_error(void) {
+    return g_error.c_str();
+}
+int evkhip_init(void) {
+    return record("init", {}, {}, {}, nullptr);
+}
+int evkhip_shutdown(void) {
+    return record("shutdown", {}, {}, {}, nullptr);
+}
+
+int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int ta, int tb, int acc,
+                  uint32_t tm, uint32_t tn, void* stream) {
+    return record("matmul", {a, b, c}, {ta, tb, acc, tm, tn}, {}, stream);
+}
+int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
+                           const evkhip_tensor* o, int causal, float* lse, void* stream) {
+    return record("flash_attention", {q, k, v, o}, {causal}, {}, stream, lse);
+}
+int evkhip_flash_attention_bwd(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
+                               const evkhip_tensor* o, const evkhip_tensor* dO, const evkhip_tensor* dQ,
+                               const evkhip_tensor* dK, const evkhip_tensor* dV, uint32_t heads, int causal,
+                               const float* lse, void* stream) {
+    return record("flash_attention_bwd", {q, k, v, o, dO, dQ, dK, dV}, {heads, causal}, {}, stream, lse);
+}
+int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* kc, const evkhip_tensor* vc,
+                                  const evkhip_tensor* out, uint32_t L, uint32_t heads, void* stream) {
+    return record("single_query_attention", {q, kc, vc, out}, {L, heads}, {}, stream);
+}
+int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream) {
+    return record("rms_norm", {in, out}, {}, {eps}, stream);
+}
+int evkhip_rope(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t b, uint32_t n, uint32_t d, float base,
+                uint32_t pos, uint32_t hd, void* stream) {
+    return record("rope", {in, out}, {b, n, d, pos, hd}, {base}, stream);
+}
+int evkhip_gelu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream) {
+    return record("gelu", {in, out}, {}, {}, stream);
+}
+// add is computed (fp32 sum rounded to fp16) so data round trips can be checked
+int evkhip_add(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, void* stream) {
+    const int s = record("add", {a, b, c}, {}, {}, stream);
+    if (s != EVKHIP_OK) return s;
+    const uint64_t n = elems(c);
+    if (elems(a) != n || elems(b) != n) return EVKHIP_ERR_SHAPE;
+    const float16_t* x = static_cast<const float16_t*>(a->data);
+    const float16_t* y = static_cast<const float16_t*>(b->data);
+    float16_t* z = static_cast<float16_t*>(c->data);
+    for (uint64_t i = 0; i < n; ++i) z[i] = float16_t(float(x[i]) + float(y[i]));
+    return EVKHIP_OK;
+}
+int evkhip_embed(const evkhip_tensor* e, const evkhip_tensor* idx, const evkhip_tensor* out, void* stream) {
+    return record("embed", {e, idx, out}, {}, {}, stream);
+}
+int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out, uint32_t position, uint16_t base,
+                         uint16_t count, void* stream) {
+    return record("greedy_sample", {logits, out}, {position, base, count}, {}, stream);
+}
+
+}  // extern "C"

@@ -50,6 +50,37 @@ def test_api_library_exports(L):
     del api
 
 
+def _api_tests_binary():
+    exe = os.path.join(ROOT, "evk_amd", "bin", "api_tests")
+    if not os.path.exists(exe):
+        pytest.fail("evk_amd/bin/api_tests is not built: run `python -m evk_amd.build`")
+    return exe
+
+
+def test_cpp_api_host_tests():
+    # float16_t and Shape of include/evk_ai.h, no GPU calls
+    import subprocess
+    r = subprocess.run([_api_tests_binary(), "--cpu"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
+
+
+def test_cpp_float16_matches_oracle(tmp_path, orc):
+    # the header's fp32->fp16 conversion bit-equals the oracle's (itself
+    # pinned to the reference's float16_t) on 2^20 patterns over all exponents
+    import subprocess
+
+    import numpy as np
+    out = tmp_path / "f16.bin"
+    r = subprocess.run([_api_tests_binary(), "--f16-sweep", str(out)], capture_output=True, timeout=120)
+    assert r.returncode == 0
+    got = np.fromfile(out, dtype=np.uint16)
+    bits = (np.arange(1 << 20, dtype=np.uint64) * 4093).astype(np.uint32)
+    want = orc.f32_to_f16(bits.view(np.float32))
+    assert got.shape == want.shape
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(hex(int(bits[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:5]]
+
+
 def T(shape, ptr=0x1000):
     import evk_amd
     return evk_amd.desc((ptr, tuple(shape)))
