@@ -24,7 +24,8 @@ __all__ = [
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libevkhip.so")
+# EVKHIP_LIBRARY points the mirror at another build of the library (same ABI)
+LIB_PATH = os.environ.get("EVKHIP_LIBRARY") or os.path.join(_HERE, "libevkhip.so")
 _LIB = None
 
 MAX_DIMS = 8

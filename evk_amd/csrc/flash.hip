@@ -434,6 +434,261 @@ __global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Forward, key-split (O and the public LSE).
+//
+// Workgroup: 64 query rows and 4 waves.  Wave w owns key chunks w, w+4, ...
+// (32 keys each) of the row tile's key range, for all 64 rows: each wave runs
+// its own online softmax over its keys and the four partial states
+// (m, l, O) are merged once at the end.  No K/V tile is shared, so nothing
+// is re-read from LDS by several waves and the main loop has no barrier:
+//   S^T(32 keys x 64 q) = K Q^T with v_mfma_f32_16x16x32_f16: the K chunk is
+//       loaded from global memory straight into A-operand registers; Q^T
+//       (64 rows) stays in B-operand registers for the whole kernel.
+//   O^T(DH x 64 q) += V^T P^T: the V chunk goes through a per-wave LDS slot
+//       and comes back transposed by ds_read_b64_tr_b16; P^T is already in
+//       B-operand order (slot s <-> key 4g+s for s < 4, 16+4g+s-4 after).
+//   row sums: ones . P^T on the MFMA.
+// The next chunk's K and V are prefetched into registers during the current
+// chunk.  Rescaling is lazy (RESCALE_LOG2), as in flash_fwd.
+// ---------------------------------------------------------------------------
+constexpr int KC = 32;  // keys per chunk
+
+// Buffer loads: the base and size live in a scalar resource, offsets past the
+// size read as zero.
+DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
+
+template <int DH>
+struct KsLayout {
+    static constexpr int KS = DH / 32;           // k-steps of QK^T
+    static constexpr int DB = DH / 16;           // dh blocks of O^T
+    static constexpr int VW = DH + 8;            // V slot row stride (halves)
+    static constexpr int VSLOT = KC * VW;        // halves per wave slot
+    static constexpr int VPER = KC * DH / 8 / 64;  // 16-byte V pieces per lane
+    static constexpr int OW = DH + 4;            // merge row stride (floats)
+    static constexpr int MERGE = 4 * 64 * OW + 2 * 4 * 64;  // floats: O partials, m, l
+    static constexpr int LDS_BYTES = (MERGE * 4 > 4 * VSLOT * 2) ? MERGE * 4 : 4 * VSLOT * 2;
+};
+
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
+    using L = KsLayout<DH>;
+    constexpr int KS = L::KS, DB = L::DB, VW = L::VW, VPER = L::VPER;
+    __shared__ __attribute__((aligned(16))) float smem_f[L::LDS_BYTES / 4];
+    f16* vslot_all = reinterpret_cast<f16*>(smem_f);
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int nrg = (NH + FR - 1) / FR;
+    int rg, b;
+    fwd_block_map(blockIdx.x, nrg, p.B, CAUSAL, round, &rg, &b);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int R0 = rg * FR;
+    const int last = min(R0 + FR - 1, NH - 1);
+    const int pmin = R0 / H, pmax = last / H;
+    const int kend = CAUSAL ? min(N, pmax + 1) : N;
+    const int nch = (kend + KC - 1) / KC;
+    const float c2 = p.scale_log2;
+
+    // K, V of this batch and Q of this row tile through buffer loads: rows
+    // past the end read as zero (such keys are masked, such rows not stored)
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const __amdgpu_buffer_rsrc_t qres =
+        buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, (uint32_t)(last - R0 + 1) * DH * 2);
+    f16* vslot = vslot_all + wave * L::VSLOT;
+
+    // Q^T B operands: query R0 + 16 qb + l16, dh [32 ks + 8 g, +8)
+    half8 qf[4][KS];
+    int qpos[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+        qpos[qb] = min(R0 + qb * 16 + l16, NH - 1) / H;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            qf[qb][ks] = as_half8(buf_load16(qres, (uint32_t)((qb * 16 + l16) * DH + ks * 32 + g * 8) * 2, 0));
+    }
+
+    floatx4 oacc[DB][4];
+    floatx4 lacc[4];
+    float m_ref[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) oacc[d][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        lacc[qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        m_ref[qb] = -INFINITY;
+    }
+    const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f,
+                         (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
+
+    // chunk registers: K A-operands (key 16 kb + l16, dh 32 ks + 8 g) and this
+    // lane's V pieces (16 bytes at byte lane*16 + i*1024 of the chunk); the
+    // chunk base is the scalar buffer offset
+    const uint32_t k_vo = (uint32_t)(l16 * DH + g * 8) * 2;
+    const uint32_t v_vo = (uint32_t)lane * 16;
+    u32x4 kr[2][KS], vr[VPER];
+    auto load_chunk = [&](int c) {
+        const uint32_t so = (uint32_t)c * KC * DH * 2;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, so);
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, so);
+    };
+
+    int c = wave;
+    if (c < nch) load_chunk(c);
+    const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    for (; c < nch; c += 4) {
+        const int key0 = c * KC;
+        half8 kf[2][KS];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) kf[kb][ks] = as_half8(kr[kb][ks]);
+        // V chunk into this wave's slot (LDS ops of a wave complete in order,
+        // so the previous chunk's transposed reads are done)
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int idx = lane + 64 * i;
+            *reinterpret_cast<u32x4*>(vslot + (idx / (DH / 8)) * VW + (idx % (DH / 8)) * 8) = vr[i];
+        }
+        if (c + 4 < nch) load_chunk(c + 4);
+
+        floatx4 s[2][4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < 4; ++qb) {
+                s[kb][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) s[kb][qb] = mfma16(kf[kb][ks], qf[qb][ks], s[kb][qb]);
+            }
+        // element j of s[kb][qb]: key key0 + 16 kb + 4 g + j, query row R0 + 16 qb + l16
+        if (key0 + KC > N || (CAUSAL && key0 + KC - 1 > pmin)) {
+#pragma unroll
+            for (int qb = 0; qb < 4; ++qb) {
+                const int lim = (CAUSAL ? min(N - 1, qpos[qb]) : N - 1) - key0 - 4 * g;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        s[kb][qb][j] = (kb * 16 + j > lim) ? -INFINITY : s[kb][qb][j];
+            }
+        }
+        float mx[4];
+        bool grow = false;
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+            mx[qb] = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
+                           fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
+            grow |= mx[qb] > m_ref[qb] + RESCALE_LOG2;
+        }
+        if (__any(grow)) {
+#pragma unroll
+            for (int qb = 0; qb < 4; ++qb) {
+                float m = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
+                m = fmaxf(m, __shfl_xor(m, 32, 64));
+                const float m_new = fmaxf(m_ref[qb], m);
+                const float alpha = (m_ref[qb] == -INFINITY) ? 0.0f : fast_exp2(m_ref[qb] - m_new);
+#pragma unroll
+                for (int d = 0; d < DB; ++d) oacc[d][qb] *= alpha;
+                lacc[qb] *= alpha;
+                m_ref[qb] = m_new;
+            }
+        }
+        half8 pb[4];
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+            const float nbase = (m_ref[qb] == -INFINITY) ? 0.0f : -m_ref[qb];
+            float e[2][4];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) e[kb][j] = fast_exp2(__builtin_fmaf(s[kb][qb][j], c2, nbase));
+            u32x4 u = {pack_h2(e[0][0], e[0][1]), pack_h2(e[0][2], e[0][3]),
+                       pack_h2(e[1][0], e[1][1]), pack_h2(e[1][2], e[1][3])};
+            pb[qb] = as_half8(u);
+            lacc[qb] = mfma16(ones8, pb[qb], lacc[qb]);
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const f16* base0 = vslot + (g * 4 + trow) * VW + d * 16 + tcol;
+            const half8 vt = cat4(lds_read_tr(base0), lds_read_tr(base0 + 16 * VW));
+#pragma unroll
+            for (int qb = 0; qb < 4; ++qb) oacc[d][qb] = mfma16(vt, pb[qb], oacc[d][qb]);
+        }
+    }
+
+    // ---- merge the four waves' partial softmax states ----
+    // Merge addresses derive from an opaque copy of the lane id, so the
+    // compiler computes them here instead of keeping them live through the loop.
+    int ml = lane;
+    asm volatile("" : "+v"(ml));
+    const int ml16 = ml & 15, mg = ml >> 4;
+    __syncthreads();  // every wave is done with its V slot
+    float* ob = smem_f;                      // [wave][64 q][OW]
+    float* mw = smem_f + 4 * 64 * L::OW;     // [wave][64]
+    float* lw = mw + 4 * 64;                 // [wave][64]
+    if (mg == 0) {
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+            mw[wave * 64 + qb * 16 + ml16] = m_ref[qb];
+            lw[wave * 64 + qb * 16 + ml16] = lacc[qb][0];
+        }
+    }
+    __syncthreads();
+    float l_tot[4], m_tot[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+        const int q = qb * 16 + ml16;
+        float m = mw[q];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) m = fmaxf(m, mw[w * 64 + q]);
+        float lt = 0.0f, mine = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mwq = mw[w * 64 + q];
+            const float a = (mwq == -INFINITY) ? 0.0f : fast_exp2(mwq - m);
+            lt += a * lw[w * 64 + q];
+            if (w == wave) mine = a;
+        }
+        m_tot[qb] = m;
+        l_tot[qb] = lt;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            *reinterpret_cast<floatx4*>(ob + (wave * 64 + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb] * mine;
+    }
+    __syncthreads();
+    // wave w finishes query block qb = w
+    const int q = wave * 16 + ml16;
+    const int row = R0 + q;
+    if (row >= NH) return;
+    const float inv_l = l_tot[wave] > 0.0f ? 1.0f / l_tot[wave] : 0.0f;
+    f16* Ob = p.out + (int64_t)b * NH * DH + (int64_t)row * DH;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+        floatx4 acc = *reinterpret_cast<const floatx4*>(ob + q * L::OW + d * 16 + mg * 4);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) acc += *reinterpret_cast<const floatx4*>(ob + (w * 64 + q) * L::OW + d * 16 + mg * 4);
+        u32x2 o = {pack_h2(acc[0] * inv_l, acc[1] * inv_l), pack_h2(acc[2] * inv_l, acc[3] * inv_l)};
+        *reinterpret_cast<u32x2*>(Ob + d * 16 + mg * 4) = o;
+    }
+    if (p.lse && mg == 0) {
+        const float lse = (l_tot[wave] > 0.0f) ? (m_tot[wave] + log2f(l_tot[wave])) * kLn2 : -INFINITY;
+        p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
+    }
+}
+
 // lse2_rows / d_rows from a saved LSE and O: D_i = rowsum(dO_i * O_i).
 template <int DH>
 __global__ __launch_bounds__(256) void flash_bwd_pre(FlashArgs p) {
@@ -838,6 +1093,14 @@ hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st)
     // zigzag round = one workgroup per CU: round r+1 runs in reverse, so the
     // workgroups that land on the same CU pair heavy with light row groups
     const int round = device_cu_count();
+    if constexpr (DH <= 64) {
+        // buffer offsets are 32-bit: one batch of K (or V) must stay below 2 GiB
+        if (mode == 0 && (int64_t)a.N * DH * 2 < (int64_t)INT32_MAX) {
+            if (causal) hipLaunchKernelGGL((flash_fwd_ks<DH, true>), grid, dim3(256), 0, st, a, round);
+            else hipLaunchKernelGGL((flash_fwd_ks<DH, false>), grid, dim3(256), 0, st, a, round);
+            return hipGetLastError();
+        }
+    }
     if (mode == 0) {
         if (causal) hipLaunchKernelGGL((flash_fwd<DH, true, 0>), grid, dim3(512), 0, st, a, round);
         else hipLaunchKernelGGL((flash_fwd<DH, false, 0>), grid, dim3(512), 0, st, a, round);
