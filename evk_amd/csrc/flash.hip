@@ -453,6 +453,9 @@ __global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
 // chunk.  Rescaling is lazy (RESCALE_LOG2), as in flash_fwd.
 // ---------------------------------------------------------------------------
 constexpr int KC = 32;  // keys per chunk
+#ifndef FWD_KS_QB
+#define FWD_KS_QB 4  // 16-row query blocks per wave (rows per workgroup / 16)
+#endif
 
 // Buffer loads: the base and size live in a scalar resource, offsets past the
 // size read as zero.
@@ -464,34 +467,36 @@ DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
 }
 
 
-template <int DH>
+template <int DH, int QB>
 struct KsLayout {
+    static constexpr int ROWS = 16 * QB;         // query rows per workgroup
     static constexpr int KS = DH / 32;           // k-steps of QK^T
     static constexpr int DB = DH / 16;           // dh blocks of O^T
     static constexpr int VW = DH + 8;            // V slot row stride (halves)
     static constexpr int VSLOT = KC * VW;        // halves per wave slot
     static constexpr int VPER = KC * DH / 8 / 64;  // 16-byte V pieces per lane
     static constexpr int OW = DH + 4;            // merge row stride (floats)
-    static constexpr int MERGE = 4 * 64 * OW + 2 * 4 * 64;  // floats: O partials, m, l
+    static constexpr int MERGE = 4 * ROWS * OW + 2 * 4 * ROWS + 2 * ROWS;  // O partials, m, l; m_tot, l_tot
     static constexpr int LDS_BYTES = (MERGE * 4 > 4 * VSLOT * 2) ? MERGE * 4 : 4 * VSLOT * 2;
 };
 
-template <int DH, bool CAUSAL>
+template <int DH, int QB, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
-    using L = KsLayout<DH>;
+    using L = KsLayout<DH, QB>;
+    constexpr int ROWS = L::ROWS;
     constexpr int KS = L::KS, DB = L::DB, VW = L::VW, VPER = L::VPER;
     __shared__ __attribute__((aligned(16))) float smem_f[L::LDS_BYTES / 4];
     f16* vslot_all = reinterpret_cast<f16*>(smem_f);
 
     const int H = p.H, N = p.N, NH = N * H;
-    const int nrg = (NH + FR - 1) / FR;
+    const int nrg = (NH + ROWS - 1) / ROWS;
     int rg, b;
     fwd_block_map(blockIdx.x, nrg, p.B, CAUSAL, round, &rg, &b);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
-    const int R0 = rg * FR;
-    const int last = min(R0 + FR - 1, NH - 1);
+    const int R0 = rg * ROWS;
+    const int last = min(R0 + ROWS - 1, NH - 1);
     const int pmin = R0 / H, pmax = last / H;
     const int kend = CAUSAL ? min(N, pmax + 1) : N;
     const int nch = (kend + KC - 1) / KC;
@@ -506,21 +511,21 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
     f16* vslot = vslot_all + wave * L::VSLOT;
 
     // Q^T B operands: query R0 + 16 qb + l16, dh [32 ks + 8 g, +8)
-    half8 qf[4][KS];
-    int qpos[4];
+    half8 qf[QB][KS];
+    int qpos[QB];
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         qpos[qb] = min(R0 + qb * 16 + l16, NH - 1) / H;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             qf[qb][ks] = as_half8(buf_load16(qres, (uint32_t)((qb * 16 + l16) * DH + ks * 32 + g * 8) * 2, 0));
     }
 
-    floatx4 oacc[DB][4];
-    floatx4 lacc[4];
-    float m_ref[4];
+    floatx4 oacc[DB][QB];
+    floatx4 lacc[QB];
+    float m_ref[QB];
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int d = 0; d < DB; ++d) oacc[d][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc[qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -564,11 +569,11 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
         }
         if (c + 4 < nch) load_chunk(c + 4);
 
-        floatx4 s[2][4];
+        floatx4 s[2][QB];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int qb = 0; qb < 4; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 s[kb][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) s[kb][qb] = mfma16(kf[kb][ks], qf[qb][ks], s[kb][qb]);
@@ -576,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
         // element j of s[kb][qb]: key key0 + 16 kb + 4 g + j, query row R0 + 16 qb + l16
         if (key0 + KC > N || (CAUSAL && key0 + KC - 1 > pmin)) {
 #pragma unroll
-            for (int qb = 0; qb < 4; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 const int lim = (CAUSAL ? min(N - 1, qpos[qb]) : N - 1) - key0 - 4 * g;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
@@ -585,17 +590,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
                         s[kb][qb][j] = (kb * 16 + j > lim) ? -INFINITY : s[kb][qb][j];
             }
         }
-        float mx[4];
+        float mx[QB];
         bool grow = false;
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             mx[qb] = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
                            fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
             grow |= mx[qb] > m_ref[qb] + RESCALE_LOG2;
         }
         if (__any(grow)) {
 #pragma unroll
-            for (int qb = 0; qb < 4; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 float m = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
                 m = fmaxf(m, __shfl_xor(m, 32, 64));
                 const float m_new = fmaxf(m_ref[qb], m);
@@ -606,9 +611,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
                 m_ref[qb] = m_new;
             }
         }
-        half8 pb[4];
+        half8 pb[QB];
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             const float nbase = (m_ref[qb] == -INFINITY) ? 0.0f : -m_ref[qb];
             float e[2][4];
 #pragma unroll
@@ -625,7 +630,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
             const f16* base0 = vslot + (g * 4 + trow) * VW + d * 16 + tcol;
             const half8 vt = cat4(lds_read_tr(base0), lds_read_tr(base0 + 16 * VW));
 #pragma unroll
-            for (int qb = 0; qb < 4; ++qb) oacc[d][qb] = mfma16(vt, pb[qb], oacc[d][qb]);
+            for (int qb = 0; qb < QB; ++qb) oacc[d][qb] = mfma16(vt, pb[qb], oacc[d][qb]);
         }
     }
 
@@ -636,56 +641,527 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
     asm volatile("" : "+v"(ml));
     const int ml16 = ml & 15, mg = ml >> 4;
     __syncthreads();  // every wave is done with its V slot
-    float* ob = smem_f;                      // [wave][64 q][OW]
-    float* mw = smem_f + 4 * 64 * L::OW;     // [wave][64]
-    float* lw = mw + 4 * 64;                 // [wave][64]
+    float* ob = smem_f;                          // [wave][ROWS][OW]
+    float* mw = smem_f + 4 * ROWS * L::OW;       // [wave][ROWS]
+    float* lw = mw + 4 * ROWS;                   // [wave][ROWS]
+    float* mt = lw + 4 * ROWS;                   // [ROWS]
+    float* lt = mt + ROWS;                       // [ROWS]
     if (mg == 0) {
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-            mw[wave * 64 + qb * 16 + ml16] = m_ref[qb];
-            lw[wave * 64 + qb * 16 + ml16] = lacc[qb][0];
+        for (int qb = 0; qb < QB; ++qb) {
+            mw[wave * ROWS + qb * 16 + ml16] = m_ref[qb];
+            lw[wave * ROWS + qb * 16 + ml16] = lacc[qb][0];
         }
     }
     __syncthreads();
-    float l_tot[4], m_tot[4];
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const int q = qb * 16 + ml16;
         float m = mw[q];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) m = fmaxf(m, mw[w * 64 + q]);
-        float lt = 0.0f, mine = 0.0f;
+        for (int w = 1; w < 4; ++w) m = fmaxf(m, mw[w * ROWS + q]);
+        const float mine = (m_ref[qb] == -INFINITY) ? 0.0f : fast_exp2(m_ref[qb] - m);
+        if (wave == 0 && mg == 0) {
+            float l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float mwq = mw[w * 64 + q];
-            const float a = (mwq == -INFINITY) ? 0.0f : fast_exp2(mwq - m);
-            lt += a * lw[w * 64 + q];
-            if (w == wave) mine = a;
+            for (int w = 0; w < 4; ++w) {
+                const float mwq = mw[w * ROWS + q];
+                l += (mwq == -INFINITY) ? 0.0f : fast_exp2(mwq - m) * lw[w * ROWS + q];
+            }
+            mt[q] = m;
+            lt[q] = l;
         }
-        m_tot[qb] = m;
-        l_tot[qb] = lt;
 #pragma unroll
         for (int d = 0; d < DB; ++d)
-            *reinterpret_cast<floatx4*>(ob + (wave * 64 + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb] * mine;
+            *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb] * mine;
     }
     __syncthreads();
-    // wave w finishes query block qb = w
-    const int q = wave * 16 + ml16;
-    const int row = R0 + q;
-    if (row >= NH) return;
-    const float inv_l = l_tot[wave] > 0.0f ? 1.0f / l_tot[wave] : 0.0f;
-    f16* Ob = p.out + (int64_t)b * NH * DH + (int64_t)row * DH;
+    // wave w finishes rows [w*ROWS/4, (w+1)*ROWS/4): a lane owns 8 dh of one row
+    constexpr int CPR = DH / 8, RPW = ROWS / 4;
+    for (int rr = ml / CPR; rr < RPW; rr += 64 / CPR) {
+        const int q = wave * RPW + rr;
+        const int row = R0 + q;
+        const int dc = (ml % CPR) * 8;
+        floatx4 a0 = *reinterpret_cast<const floatx4*>(ob + q * L::OW + dc);
+        floatx4 a1 = *reinterpret_cast<const floatx4*>(ob + q * L::OW + dc + 4);
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-        floatx4 acc = *reinterpret_cast<const floatx4*>(ob + q * L::OW + d * 16 + mg * 4);
-#pragma unroll
-        for (int w = 1; w < 4; ++w) acc += *reinterpret_cast<const floatx4*>(ob + (w * 64 + q) * L::OW + d * 16 + mg * 4);
-        u32x2 o = {pack_h2(acc[0] * inv_l, acc[1] * inv_l), pack_h2(acc[2] * inv_l, acc[3] * inv_l)};
-        *reinterpret_cast<u32x2*>(Ob + d * 16 + mg * 4) = o;
+        for (int w = 1; w < 4; ++w) {
+            a0 += *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc);
+            a1 += *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc + 4);
+        }
+        const float l = lt[q];
+        const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+        if (row < NH) {
+            u32x4 o = {pack_h2(a0[0] * inv_l, a0[1] * inv_l), pack_h2(a0[2] * inv_l, a0[3] * inv_l),
+                       pack_h2(a1[0] * inv_l, a1[1] * inv_l), pack_h2(a1[2] * inv_l, a1[3] * inv_l)};
+            *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
+            if (p.lse && dc == 0) {
+                const float lse = l > 0.0f ? (mt[q] + log2f(l)) * kLn2 : -INFINITY;
+                p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
+            }
+        }
     }
-    if (p.lse && mg == 0) {
-        const float lse = (l_tot[wave] > 0.0f) ? (m_tot[wave] + log2f(l_tot[wave])) * kLn2 : -INFINITY;
-        p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
+}
+
+// ---------------------------------------------------------------------------
+// Backward dK, dV for head dims 32 and 64.
+//
+// Workgroup: 4 waves and 128 keys; wave w owns keys [32w, 32w+32) of the
+// block, with K^T and V^T as B-operand registers for the whole kernel.  The
+// workgroup walks 32-row chunks of the flattened (position, head) query rows,
+// so the MQA sum over heads happens inside the MFMA accumulation.  A chunk
+// (Q and dO rows, lse2 and D) is staged once in LDS for all four waves:
+//   S = Q K^T, dP = dO V^T (16 rows x 16 keys per v_mfma_f32_16x16x32_f16,
+//       A = rows read from LDS): lane owns one key, 4 rows per 16-row block
+//   P = 2^(S*scale*log2e - lse2_row), dS = P (dP - D_row)
+//   dV += P^T dO, dK += dS^T Q: the probabilities of two 16-row blocks are
+//       the A operand as they are (slot s <-> row 4g+s, 16+4g+s-4), and dO, Q
+//       come transposed from the LDS chunk through ds_read_b64_tr_b16.
+// The query rows of a key block are split into parts of at most PART_CHUNKS
+// chunks, one part per workgroup, so that causal key blocks near the start
+// (which see every row) do not serialise the grid.  A key block with one
+// part writes dK, dV directly; otherwise every part stores an fp32 partial
+// and flash_bwd_kv_reduce sums them in part order (deterministic).
+// ---------------------------------------------------------------------------
+typedef int intx4 __attribute__((ext_vector_type(4)));
+
+constexpr int BKB = 128;       // keys per workgroup (4 waves x 32)
+constexpr int BRC = 32;        // flattened query rows per chunk
+constexpr int PART_CHUNKS = 12;
+
+// Chunks of flattened rows that key block kb of a batch interacts with.
+__host__ __device__ inline int bwd_kv_chunks(int kb, int N, int H, bool causal) {
+    const int64_t r_lo = causal ? (int64_t)kb * BKB * H : 0;
+    return (int)(((int64_t)N * H - r_lo + BRC - 1) / BRC);
+}
+__host__ __device__ inline int bwd_kv_parts(int kb, int N, int H, bool causal) {
+    return (bwd_kv_chunks(kb, N, H, causal) + PART_CHUNKS - 1) / PART_CHUNKS;
+}
+
+template <int DH>
+struct KvLayout {
+    static constexpr int RW = DH + 8;             // chunk row stride (halves)
+    static constexpr int CHUNK = BRC * RW;        // halves per Q (or dO) chunk
+    static constexpr int STAGE = 2 * CHUNK;       // Q and dO
+    static constexpr int STATS = 2 * BRC;         // floats: lse2, D per row
+};
+
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_bwd_kv(FlashArgs p, float* part_ws, int parts_per_batch) {
+    using L = KvLayout<DH>;
+    constexpr int KS = DH / 32, DB = DH / 16, RW = L::RW;
+    constexpr int PIECES = BRC * DH / 8;              // 16-byte pieces of a chunk
+    constexpr int PPT = (2 * PIECES + 255) / 256;     // per thread (Q and dO)
+    __shared__ __attribute__((aligned(16))) f16 chunk_s[2 * L::STAGE];
+    __shared__ __attribute__((aligned(16))) float stats_s[2 * L::STATS];
+    __shared__ __attribute__((aligned(16))) int pos_s[2 * BRC];  // position of each row
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int nkb = (N + BKB - 1) / BKB;
+    // workgroup -> (batch, key block, part); heavy key blocks first
+    const int b = blockIdx.x / parts_per_batch;
+    int rem = blockIdx.x % parts_per_batch, kb = 0, nparts = 0, slot0 = 0;
+    for (; kb < nkb; ++kb) {
+        nparts = bwd_kv_parts(kb, N, H, CAUSAL);
+        if (rem < nparts) break;
+        rem -= nparts;
+        slot0 += nparts;
+    }
+    const int part = rem;
+    const int nch_all = bwd_kv_chunks(kb, N, H, CAUSAL);
+    const int c_lo = part * PART_CHUNKS, c_hi = min(nch_all, c_lo + PART_CHUNKS);
+    const int r_lo = CAUSAL ? kb * BKB * H : 0;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int k0 = kb * BKB + wave * 32;  // this wave's first key
+    const float c2 = p.scale_log2;
+
+    // K^T, V^T B operands: key k0 + 16 kb2 + l16, dh [32 ks + 8 g, +8)
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    half8 kt[2][KS], vt[2][KS];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const uint32_t off = (uint32_t)((k0 + 16 * k2 + l16) * DH + ks * 32 + g * 8) * 2;
+            kt[k2][ks] = as_half8(buf_load16(kres, off, 0));
+            vt[k2][ks] = as_half8(buf_load16(vres, off, 0));
+        }
+
+    floatx4 dk[2][DB], dv[2][DB];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            dk[k2][d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            dv[k2][d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    // chunk staging: thread t moves 16-byte pieces t, t+256, ... of [Q rows | dO rows]
+    const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
+    const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
+    const __amdgpu_buffer_rsrc_t lres = buf_rsrc(p.lse2_rows + (int64_t)b * NH, (uint32_t)NH * 4);
+    const __amdgpu_buffer_rsrc_t dres = buf_rsrc(p.d_rows + (int64_t)b * NH, (uint32_t)NH * 4);
+    u32x4 pr[PPT];
+    float sr = 0.0f;
+    int spos = 0;
+    auto gload = [&](int c) {
+        const uint32_t row0 = (uint32_t)(r_lo + c * BRC);
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            const int which = pc / PIECES, pi = pc % PIECES;
+            const uint32_t off = (row0 * DH + pi * 8) * 2;
+            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES)
+                pr[i] = buf_load16(which ? gres : qres, off, 0);
+        }
+        if (threadIdx.x < 2 * BRC) {
+            const int which = threadIdx.x / BRC, r = threadIdx.x % BRC;
+            sr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(which ? dres : lres,
+                                                                                 (row0 + r) * 4, 0, 0));
+        } else if (threadIdx.x < 3 * BRC) {
+            spos = (int)((row0 + threadIdx.x - 2 * BRC) / (uint32_t)H);
+        }
+    };
+    auto lstore = [&](int stage) {
+        f16* cs = chunk_s + stage * L::STAGE;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            const int which = pc / PIECES, pi = pc % PIECES;
+            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES)
+                *reinterpret_cast<u32x4*>(cs + which * L::CHUNK + (pi / (DH / 8)) * RW + (pi % (DH / 8)) * 8) = pr[i];
+        }
+        if (threadIdx.x < 2 * BRC) stats_s[stage * L::STATS + threadIdx.x] = sr;
+        else if (threadIdx.x < 3 * BRC) pos_s[stage * BRC + threadIdx.x - 2 * BRC] = spos;
+    };
+
+    if (c_lo < c_hi) {
+        gload(c_lo);
+        lstore(0);
+    }
+    __syncthreads();
+    const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    for (int c = c_lo; c < c_hi; ++c) {
+        const int stage = (c - c_lo) & 1;
+        if (c + 1 < c_hi) gload(c + 1);
+        const int row0 = r_lo + c * BRC;
+        // rows of this chunk hold positions row0/H .. (row0+31)/H
+        const bool live = !CAUSAL || (row0 + BRC - 1) / H >= k0;
+        if (live && k0 < N) {
+            const f16* qs = chunk_s + stage * L::STAGE;
+            const f16* gs = qs + L::CHUNK;
+            const float* st = stats_s + stage * L::STATS;
+            floatx4 s[2][2], dp[2][2];  // [row block][key block]
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                half8 qa[KS], ga[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    qa[ks] = *reinterpret_cast<const half8*>(qs + (rb * 16 + l16) * RW + ks * 32 + g * 8);
+                    ga[ks] = *reinterpret_cast<const half8*>(gs + (rb * 16 + l16) * RW + ks * 32 + g * 8);
+                }
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    s[rb][k2] = mfma16(qa[0], kt[k2][0], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                    dp[rb][k2] = mfma16(ga[0], vt[k2][0], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+                    for (int ks = 1; ks < KS; ++ks) {
+                        s[rb][k2] = mfma16(qa[ks], kt[k2][ks], s[rb][k2]);
+                        dp[rb][k2] = mfma16(ga[ks], vt[k2][ks], dp[rb][k2]);
+                    }
+                }
+            }
+            // element j of s[rb][k2]: row row0 + 16 rb + 4 g + j, key k0 + 16 k2 + l16
+            // masking only where some key of this wave can exceed some row's
+            // position (or lie past N)
+            const int* ps_ = pos_s + stage * BRC;
+            const int pos_min = ps_[0];
+            const bool edge = (CAUSAL && pos_min < k0 + 31) || k0 + 31 >= N;
+            half8 pa[2], da[2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const int key = k0 + 16 * k2 + l16;
+                float pv[2][4], dsv[2][4];
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) {
+                    const floatx4 l2 = *reinterpret_cast<const floatx4*>(st + rb * 16 + 4 * g);
+                    const floatx4 dd = *reinterpret_cast<const floatx4*>(st + BRC + rb * 16 + 4 * g);
+                    const intx4 ps = *reinterpret_cast<const intx4*>(ps_ + rb * 16 + 4 * g);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float pe = fast_exp2(__builtin_fmaf(s[rb][k2][j], c2, -l2[j]));
+                        if (edge && ((CAUSAL && key > ps[j]) || key >= N)) pe = 0.0f;
+                        pv[rb][j] = pe;
+                        dsv[rb][j] = pe * (dp[rb][k2][j] - dd[j]);
+                    }
+                }
+                u32x4 u = {pack_h2(pv[0][0], pv[0][1]), pack_h2(pv[0][2], pv[0][3]),
+                           pack_h2(pv[1][0], pv[1][1]), pack_h2(pv[1][2], pv[1][3])};
+                u32x4 w = {pack_h2(dsv[0][0], dsv[0][1]), pack_h2(dsv[0][2], dsv[0][3]),
+                           pack_h2(dsv[1][0], dsv[1][1]), pack_h2(dsv[1][2], dsv[1][3])};
+                pa[k2] = as_half8(u);
+                da[k2] = as_half8(w);
+            }
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const f16* gb = gs + (g * 4 + trow) * RW + d * 16 + tcol;
+                const f16* qb_ = qs + (g * 4 + trow) * RW + d * 16 + tcol;
+                const half8 gt = cat4(lds_read_tr(gb), lds_read_tr(gb + 16 * RW));
+                const half8 qt = cat4(lds_read_tr(qb_), lds_read_tr(qb_ + 16 * RW));
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    dv[k2][d] = mfma16(pa[k2], gt, dv[k2][d]);
+                    dk[k2][d] = mfma16(da[k2], qt, dk[k2][d]);
+                }
+            }
+        }
+        if (c + 1 < c_hi) lstore(stage ^ 1);
+        __syncthreads();
+    }
+
+    // element j of dk[k2][d]: key k0 + 16 k2 + 4 g + j, dh 16 d + l16
+    auto store_f16 = [&](const floatx4 (&acc)[2][DB], f16* out, float scale) {
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int key = k0 + 16 * k2 + 4 * g + j;
+                if (key < N) {
+#pragma unroll
+                    for (int d = 0; d < DB; ++d)
+                        out[((int64_t)b * N + key) * DH + d * 16 + l16] = (f16)(acc[k2][d][j] * scale);
+                }
+            }
+    };
+    if (nparts == 1) {
+        store_f16(dk, p.dK, p.scale);
+        store_f16(dv, p.dV, 1.0f);
+        return;
+    }
+    // fp32 partial of this part, lane-major: [slot][wave][dk|dv][k2][d][lane] floatx4
+    constexpr int PW = 2 * 2 * DB;
+    const int64_t slot = (int64_t)b * parts_per_batch + slot0 + part;
+    floatx4* mine = reinterpret_cast<floatx4*>(part_ws) + (slot * 4 + wave) * PW * 64;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            mine[((0 * 2 + k2) * DB + d) * 64 + lane] = dk[k2][d];
+            mine[((1 * 2 + k2) * DB + d) * 64 + lane] = dv[k2][d];
+        }
+}
+
+// Sums the fp32 partials of key blocks with several row parts, in part
+// order, and writes dK (times the softmax scale) and dV.  Grid: one
+// workgroup per (batch, key block) x 16 slices of its 4096 floatx4.
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_bwd_kv_reduce(FlashArgs p, const float* part_ws, int parts_per_batch) {
+    constexpr int DB = DH / 16, PW = 2 * 2 * DB, SLOT = 4 * PW * 64;  // floatx4 per slot
+    const int N = p.N, H = p.H;
+    const int nkb = (N + BKB - 1) / BKB;
+    const int bk = blockIdx.x / 16, slice = blockIdx.x % 16;
+    const int b = bk / nkb, kb = bk % nkb;
+    int slot0 = 0;
+    for (int k = 0; k < kb; ++k) slot0 += bwd_kv_parts(k, N, H, CAUSAL);
+    const int nparts = bwd_kv_parts(kb, N, H, CAUSAL);
+    if (nparts == 1) return;  // written directly by its only part
+    for (int e = slice * 256 + threadIdx.x; e < SLOT; e += 16 * 256) {
+        const floatx4* src = reinterpret_cast<const floatx4*>(part_ws) + ((int64_t)b * parts_per_batch + slot0) * SLOT + e;
+        floatx4 acc = src[0];
+        for (int q = 1; q < nparts; ++q) acc += src[(int64_t)q * SLOT];
+        // e = ((wave * 2 + which) * 2 + k2) * DB + d) * 64 + lane
+        const int lane = e % 64, d = (e / 64) % DB, k2 = (e / (64 * DB)) % 2, which = (e / (64 * DB * 2)) % 2,
+                  wave = e / (64 * PW);
+        const int key0 = kb * BKB + wave * 32 + 16 * k2 + 4 * (lane >> 4);
+        const int dh = d * 16 + (lane & 15);
+        f16* out = which ? p.dV : p.dK;
+        const float sc = which ? 1.0f : p.scale;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (key0 + j < N) out[((int64_t)b * N + key0 + j) * DH + dh] = (f16)(acc[j] * sc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward dQ for head dims 32 and 64: the key-split forward's structure
+// without the online softmax (P comes from the saved row statistics).
+// Workgroup: 64 flattened query rows, 4 waves; wave w takes 32-key chunks
+// w, w+4, ... for all 64 rows:
+//   S^T = K Q^T, dP^T = V dO^T (K and V chunks straight into A-operand
+//       registers; Q^T, dO^T held as B operands)
+//   P^T = 2^(S^T*scale*log2e - lse2), dS^T = P^T (dP^T - D)
+//   dQ^T += K^T dS^T: K goes through a per-wave LDS slot and comes back
+//       transposed (ds_read_b64_tr_b16); dS^T is already in B-operand order.
+// The four partial dQ^T are summed through LDS and scaled by the softmax
+// scale.
+// ---------------------------------------------------------------------------
+template <int DH>
+struct DqLayout {
+    static constexpr int KW = DH + 8;             // K slot row stride (halves)
+    static constexpr int KSLOT = KC * KW;         // halves per wave slot
+    static constexpr int OW = DH + 4;             // merge row stride (floats)
+    static constexpr int MERGE = 4 * 64 * OW;     // floats
+    static constexpr int LDS_BYTES = (MERGE * 4 > 4 * KSLOT * 2) ? MERGE * 4 : 4 * KSLOT * 2;
+};
+
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
+    using L = DqLayout<DH>;
+    constexpr int KS = DH / 32, DB = DH / 16, KW = L::KW, OW = L::OW;
+    constexpr int KPER = KC * DH / 8 / 64;  // 16-byte K pieces per lane
+    __shared__ __attribute__((aligned(16))) float smem_f[L::LDS_BYTES / 4];
+    f16* kslot = reinterpret_cast<f16*>(smem_f) + (threadIdx.x >> 6) * L::KSLOT;
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int nrg = (NH + 63) / 64;
+    const int b = blockIdx.x % p.B;
+    const int rg = CAUSAL ? nrg - 1 - blockIdx.x / p.B : blockIdx.x / p.B;  // heavy rows first
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int R0 = rg * 64;
+    const int last = min(R0 + 63, NH - 1);
+    const int pmin = R0 / H, pmax = last / H;
+    const int kend = CAUSAL ? min(N, pmax + 1) : N;
+    const int nch = (kend + KC - 1) / KC;
+    const float c2 = p.scale_log2;
+
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const uint32_t rows_bytes = (uint32_t)(last - R0 + 1) * DH * 2;
+    const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, rows_bytes);
+    const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + ((int64_t)b * NH + R0) * DH, rows_bytes);
+
+    // B operands: row R0 + 16 qb + l16, dh [32 ks + 8 g, +8); row statistics
+    half8 qf[4][KS], gf[4][KS];
+    float l2[4], dd[4];
+    int qpos[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+        const int row = min(R0 + qb * 16 + l16, NH - 1);
+        qpos[qb] = row / H;
+        l2[qb] = p.lse2_rows[(int64_t)b * NH + row];
+        dd[qb] = p.d_rows[(int64_t)b * NH + row];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const uint32_t off = (uint32_t)((qb * 16 + l16) * DH + ks * 32 + g * 8) * 2;
+            qf[qb][ks] = as_half8(buf_load16(qres, off, 0));
+            gf[qb][ks] = as_half8(buf_load16(gres, off, 0));
+        }
+    }
+    floatx4 acc[DB][4];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) acc[d][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const uint32_t a_vo = (uint32_t)(l16 * DH + g * 8) * 2;  // + k2*16*DH*2 + ks*64
+    const uint32_t p_vo = (uint32_t)lane * 16;                // + i*1024
+    const int k_lo = (lane / (DH / 8)) * KW + (lane % (DH / 8)) * 8;
+    u32x4 kp[KPER], va[2][KS];
+    auto load_chunk = [&](int c) {
+        const uint32_t so = (uint32_t)c * KC * DH * 2;
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) kp[i] = buf_load16(kres, p_vo + i * 1024, so);
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) va[k2][ks] = buf_load16(vres, a_vo + k2 * 16 * DH * 2 + ks * 64, so);
+    };
+    const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    int c = wave;
+    if (c < nch) load_chunk(c);
+    for (; c < nch; c += 4) {
+        const int key0 = c * KC;
+        // K chunk into this wave's slot; its A operands and K^T come back from LDS
+#pragma unroll
+        for (int i = 0; i < KPER; ++i)
+            *reinterpret_cast<u32x4*>(kslot + k_lo + i * (64 / (DH / 8)) * KW) = kp[i];
+        half8 vf[2][KS];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) vf[k2][ks] = as_half8(va[k2][ks]);
+        half8 kf[2][KS];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                kf[k2][ks] = *reinterpret_cast<const half8*>(kslot + (k2 * 16 + l16) * KW + ks * 32 + g * 8);
+        if (c + 4 < nch) load_chunk(c + 4);
+        half8 db_[4];
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+            floatx4 s[2], dp[2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                s[k2] = mfma16(kf[k2][0], qf[qb][0], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+                dp[k2] = mfma16(vf[k2][0], gf[qb][0], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+                for (int ks = 1; ks < KS; ++ks) {
+                    s[k2] = mfma16(kf[k2][ks], qf[qb][ks], s[k2]);
+                    dp[k2] = mfma16(vf[k2][ks], gf[qb][ks], dp[k2]);
+                }
+            }
+            // element j of s[k2]: key key0 + 16 k2 + 4 g + j, row R0 + 16 qb + l16
+            const int lim = (CAUSAL ? min(N - 1, qpos[qb]) : N - 1) - key0 - 4 * g;
+            const bool edge = key0 + KC > N || (CAUSAL && key0 + KC - 1 > pmin);
+            float dsv[2][4];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float pe = fast_exp2(__builtin_fmaf(s[k2][j], c2, -l2[qb]));
+                    if (edge && k2 * 16 + j > lim) pe = 0.0f;
+                    dsv[k2][j] = pe * (dp[k2][j] - dd[qb]);
+                }
+            u32x4 u = {pack_h2(dsv[0][0], dsv[0][1]), pack_h2(dsv[0][2], dsv[0][3]),
+                       pack_h2(dsv[1][0], dsv[1][1]), pack_h2(dsv[1][2], dsv[1][3])};
+            db_[qb] = as_half8(u);
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const f16* base0 = kslot + (g * 4 + trow) * KW + d * 16 + tcol;
+            const half8 kt = cat4(lds_read_tr(base0), lds_read_tr(base0 + 16 * KW));
+#pragma unroll
+            for (int qb = 0; qb < 4; ++qb) acc[d][qb] = mfma16(kt, db_[qb], acc[d][qb]);
+        }
+    }
+
+    // sum the four waves' dQ^T through LDS
+    int ml = lane;
+    asm volatile("" : "+v"(ml));
+    const int ml16 = ml & 15, mg = ml >> 4;
+    __syncthreads();
+    float* ob = smem_f;
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            *reinterpret_cast<floatx4*>(ob + (wave * 64 + qb * 16 + ml16) * OW + d * 16 + mg * 4) = acc[d][qb];
+    __syncthreads();
+    constexpr int CPR = DH / 8;
+    for (int rr = ml / CPR; rr < 16; rr += 64 / CPR) {
+        const int q = wave * 16 + rr;
+        const int row = R0 + q;
+        const int dc = (ml % CPR) * 8;
+        floatx4 a0 = *reinterpret_cast<const floatx4*>(ob + q * OW + dc);
+        floatx4 a1 = *reinterpret_cast<const floatx4*>(ob + q * OW + dc + 4);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            a0 += *reinterpret_cast<const floatx4*>(ob + (w * 64 + q) * OW + dc);
+            a1 += *reinterpret_cast<const floatx4*>(ob + (w * 64 + q) * OW + dc + 4);
+        }
+        if (row < NH) {
+            const float sc = p.scale;
+            u32x4 o = {pack_h2(a0[0] * sc, a0[1] * sc), pack_h2(a0[2] * sc, a0[3] * sc),
+                       pack_h2(a1[0] * sc, a1[1] * sc), pack_h2(a1[2] * sc, a1[3] * sc)};
+            *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
+        }
     }
 }
 
@@ -1083,8 +1559,10 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_scalar(FlashArgs p, int Dh)
 }
 
 // Workspace for the backward statistics (grow-only).
-float* g_bwd_ws = nullptr;
-size_t g_bwd_ws_elems = 0;
+// Backward workspace (grow-only byte arena): row statistics, fp32 dK/dV
+// partials, and O / LSE of a recomputed forward.
+char* g_bwd_ws = nullptr;
+size_t g_bwd_ws_bytes = 0;
 
 template <int DH>
 hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st) {
@@ -1096,8 +1574,10 @@ hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st)
     if constexpr (DH <= 64) {
         // buffer offsets are 32-bit: one batch of K (or V) must stay below 2 GiB
         if (mode == 0 && (int64_t)a.N * DH * 2 < (int64_t)INT32_MAX) {
-            if (causal) hipLaunchKernelGGL((flash_fwd_ks<DH, true>), grid, dim3(256), 0, st, a, round);
-            else hipLaunchKernelGGL((flash_fwd_ks<DH, false>), grid, dim3(256), 0, st, a, round);
+            constexpr int QB = FWD_KS_QB;
+            dim3 gk((unsigned)(((int64_t)a.N * a.H + 16 * QB - 1) / (16 * QB) * a.B));
+            if (causal) hipLaunchKernelGGL((flash_fwd_ks<DH, QB, true>), gk, dim3(256), 0, st, a, round);
+            else hipLaunchKernelGGL((flash_fwd_ks<DH, QB, false>), gk, dim3(256), 0, st, a, round);
             return hipGetLastError();
         }
     }
@@ -1133,12 +1613,35 @@ hipError_t launch_bwd(const FlashArgs& a, bool causal, bool have_lse, hipStream_
     return hipGetLastError();
 }
 
+// dK/dV by key blocks and row parts, then dQ by row tiles (head dims 32, 64).
+template <int DH>
+hipError_t launch_bwd_split(const FlashArgs& a, bool causal, float* parts, int parts_per_batch,
+                            hipStream_t st) {
+    const int NH = a.N * a.H;
+    dim3 gp((unsigned)(((int64_t)a.B * NH + 255) / 256));
+    hipLaunchKernelGGL(flash_bwd_pre<DH>, gp, dim3(256), 0, st, a);
+    dim3 gkv((unsigned)(a.B * parts_per_batch));
+    dim3 gq((unsigned)((NH + 63) / 64 * a.B));
+    const int nkb = (a.N + BKB - 1) / BKB;
+    dim3 gr((unsigned)(a.B * nkb * 16));
+    if (causal) {
+        hipLaunchKernelGGL((flash_bwd_kv<DH, true>), gkv, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_kv_reduce<DH, true>), gr, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_q<DH, true>), gq, dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((flash_bwd_kv<DH, false>), gkv, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_kv_reduce<DH, false>), gr, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_q<DH, false>), gq, dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 void flash_free_workspace() {
     if (g_bwd_ws) (void)hipFree(g_bwd_ws);
     g_bwd_ws = nullptr;
-    g_bwd_ws_elems = 0;
+    g_bwd_ws_bytes = 0;
 }
 
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
@@ -1160,20 +1663,51 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
     a.scale = 1.0f / sqrtf((float)dh);
     a.scale_log2 = a.scale * kLog2e;
     const size_t rows = (size_t)a.B * a.N * a.H;
-    if (2 * rows > g_bwd_ws_elems) {
+    const bool have_lse = a.lse != nullptr;
+    const bool split = mfma && dh <= 64 && (int64_t)a.N * a.H * dh * 2 < (int64_t)INT32_MAX;
+    // arena layout (256-byte aligned pieces)
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int nkb = (a.N + BKB - 1) / BKB;
+    int parts_per_batch = 0;
+    if (split)
+        for (int kb = 0; kb < nkb; ++kb) parts_per_batch += bwd_kv_parts(kb, a.N, a.H, causal);
+    const size_t stats_b = al(2 * rows * sizeof(float));
+    const size_t part_b = split ? al((size_t)a.B * parts_per_batch * 4 * (2 * 2 * (dh / 16)) * 64 * 16) : 0;
+    const size_t fwd_b = (split && !have_lse) ? al(rows * dh * 2) + al(rows * sizeof(float)) : 0;
+    const size_t need = stats_b + part_b + fwd_b;
+    if (need > g_bwd_ws_bytes) {
         if (g_bwd_ws) EVK_HIP(hipFree(g_bwd_ws));
         g_bwd_ws = nullptr;
-        EVK_HIP(hipMalloc(&g_bwd_ws, 2 * rows * sizeof(float)));
-        g_bwd_ws_elems = 2 * rows;
+        g_bwd_ws_bytes = 0;
+        EVK_HIP(hipMalloc(&g_bwd_ws, need));
+        g_bwd_ws_bytes = need;
     }
-    a.lse2_rows = g_bwd_ws;
-    a.d_rows = g_bwd_ws + rows;
-    const bool have_lse = a.lse != nullptr;
+    a.lse2_rows = reinterpret_cast<float*>(g_bwd_ws);
+    a.d_rows = a.lse2_rows + rows;
     hipError_t e;
-    if (mfma && dh == 32) e = launch_bwd<32>(a, causal, have_lse, st);
-    else if (mfma && dh == 64) e = launch_bwd<64>(a, causal, have_lse, st);
-    else if (mfma && dh == 128) e = launch_bwd<128>(a, causal, have_lse, st);
-    else {
+    if (split) {
+        float* parts = reinterpret_cast<float*>(g_bwd_ws + stats_b);
+        if (!have_lse) {
+            // recompute the forward's O and LSE into the arena
+            FlashArgs f = a;
+            f16* o_ws = reinterpret_cast<f16*>(g_bwd_ws + stats_b + part_b);
+            float* l_ws = reinterpret_cast<float*>(g_bwd_ws + stats_b + part_b + al(rows * dh * 2));
+            f.out = o_ws;
+            f.lse = l_ws;
+            e = (dh == 32) ? launch_fwd<32>(f, causal, 0, st) : launch_fwd<64>(f, causal, 0, st);
+            if (e != hipSuccess) return check_hip(e, "flash backward: forward recompute");
+            a.o = o_ws;
+            a.lse = l_ws;
+        }
+        e = (dh == 32) ? launch_bwd_split<32>(a, causal, parts, parts_per_batch, st)
+                       : launch_bwd_split<64>(a, causal, parts, parts_per_batch, st);
+    } else if (mfma && dh == 32) {
+        e = launch_bwd<32>(a, causal, have_lse, st);
+    } else if (mfma && dh == 64) {
+        e = launch_bwd<64>(a, causal, have_lse, st);
+    } else if (mfma && dh == 128) {
+        e = launch_bwd<128>(a, causal, have_lse, st);
+    } else {
         dim3 g((unsigned)((rows + 63) / 64));
         if (have_lse) {
             hipLaunchKernelGGL(flash_bwd_pre_scalar, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
