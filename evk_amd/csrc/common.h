@@ -84,6 +84,15 @@ DEV void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
     }
 }
 
+// Raw buffer loads: a descriptor over [base, base + bytes); a 16-byte load
+// at byte offset voff + soff past the end returns zeros.
+DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 DEV float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -93,6 +102,25 @@ DEV float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// tanh GELU of gelu.comp (evk_ai.cpp:679-699)
+DEV float gelu_f(float x) {
+    const float ka = 0.7978845608028654f, kb = 0.044715f;
+    float u = ka * (x + kb * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+
+// greedy_sample.comp's winner is the maximum under the total order
+// (value desc, bitrev8(j mod 256) asc, j asc); rank encodes the last two.
+DEV uint32_t greedy_rank(uint32_t j) {
+    return ((__builtin_bitreverse32(j & 255u) >> 24) << 16) | (j >> 8);
+}
+DEV uint32_t greedy_index(uint32_t rank) {
+    return ((rank & 0xFFFFu) << 8) | (__builtin_bitreverse32(rank >> 16) >> 24);
+}
+DEV bool greedy_better(float va, uint32_t ra, float vb, uint32_t rb) {
+    return va > vb || (va == vb && ra < rb);
 }
 
 DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(f16, h); }

@@ -235,11 +235,6 @@ __global__ __launch_bounds__(256) void rope_k(const f16* in, f16* out, int B, in
     out[idx + 1] = (f16)(x0 * s + x1 * c);
 }
 
-DEV float gelu_f(float x) {
-    const float ka = 0.7978845608028654f, kb = 0.044715f;
-    float u = ka * (x + kb * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(u));
-}
 
 __global__ __launch_bounds__(256) void gelu_k(const f16* in, f16* out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -267,12 +262,6 @@ __global__ __launch_bounds__(256) void embed_k(const f16* table, const uint16_t*
 // (value > -FLT_MAX), j = token - token_base; with no valid candidate it is
 // token_base.  Any reduction tree over this order gives the same winner.
 // ---------------------------------------------------------------------------
-DEV uint32_t greedy_rank(uint32_t j) {
-    return ((__builtin_bitreverse32(j & 255u) >> 24) << 16) | (j >> 8);
-}
-DEV bool greedy_better(float va, uint32_t ra, float vb, uint32_t rb) {
-    return va > vb || (va == vb && ra < rb);
-}
 
 __global__ __launch_bounds__(256) void greedy_k(const f16* logits, uint16_t* out, int S, int V, int position,
                                                  int token_base, int token_count) {

@@ -459,12 +459,6 @@ constexpr int KC = 32;  // keys per chunk
 
 // Buffer loads: the base and size live in a scalar resource, offsets past the
 // size read as zero.
-DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
 
 
 template <int DH, int QB>
@@ -504,8 +498,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
 
     // K, V of this batch and Q of this row tile through buffer loads: rows
     // past the end read as zero (such keys are masked, such rows not stored)
-    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
-    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const f16* kb_ptr = p.k + (int64_t)b * N * DH;
+    const f16* vb_ptr = p.v + (int64_t)b * N * DH;
     const __amdgpu_buffer_rsrc_t qres =
         buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, (uint32_t)(last - R0 + 1) * DH * 2);
     f16* vslot = vslot_all + wave * L::VSLOT;
@@ -535,19 +529,22 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
                          (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
 
     // chunk registers: K A-operands (key 16 kb + l16, dh 32 ks + 8 g) and this
-    // lane's V pieces (16 bytes at byte lane*16 + i*1024 of the chunk); the
-    // chunk base is the scalar buffer offset
+    // lane's V pieces (16 bytes at byte lane*16 + i*1024 of the chunk).  Each
+    // chunk gets descriptors over its own keys [c*KC, N), so keys past N read
+    // as zeros.
     const uint32_t k_vo = (uint32_t)(l16 * DH + g * 8) * 2;
     const uint32_t v_vo = (uint32_t)lane * 16;
     u32x4 kr[2][KS], vr[VPER];
     auto load_chunk = [&](int c) {
-        const uint32_t so = (uint32_t)c * KC * DH * 2;
+        const uint32_t rem = (uint32_t)(N - c * KC) * DH * 2;
+        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (int64_t)c * KC * DH, rem);
+        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (int64_t)c * KC * DH, rem);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, so);
+            for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, 0);
 #pragma unroll
-        for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, so);
+        for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, 0);
     };
 
     int c = wave;
@@ -1030,8 +1027,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
     const int nch = (kend + KC - 1) / KC;
     const float c2 = p.scale_log2;
 
-    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
-    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2);
+    const f16* kb_ptr = p.k + (int64_t)b * N * DH;
+    const f16* vb_ptr = p.v + (int64_t)b * N * DH;
     const uint32_t rows_bytes = (uint32_t)(last - R0 + 1) * DH * 2;
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, rows_bytes);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + ((int64_t)b * NH + R0) * DH, rows_bytes);
@@ -1063,14 +1060,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
     const uint32_t p_vo = (uint32_t)lane * 16;                // + i*1024
     const int k_lo = (lane / (DH / 8)) * KW + (lane % (DH / 8)) * 8;
     u32x4 kp[KPER], va[2][KS];
-    auto load_chunk = [&](int c) {
-        const uint32_t so = (uint32_t)c * KC * DH * 2;
+    auto load_chunk = [&](int c) {  // descriptors over keys [c*KC, N): keys past N read as zeros
+        const uint32_t rem = (uint32_t)(N - c * KC) * DH * 2;
+        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (int64_t)c * KC * DH, rem);
+        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (int64_t)c * KC * DH, rem);
 #pragma unroll
-        for (int i = 0; i < KPER; ++i) kp[i] = buf_load16(kres, p_vo + i * 1024, so);
+        for (int i = 0; i < KPER; ++i) kp[i] = buf_load16(kres, p_vo + i * 1024, 0);
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) va[k2][ks] = buf_load16(vres, a_vo + k2 * 16 * DH * 2 + ks * 64, so);
+            for (int ks = 0; ks < KS; ++ks) va[k2][ks] = buf_load16(vres, a_vo + k2 * 16 * DH * 2 + ks * 64, 0);
     };
     const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
     int c = wave;

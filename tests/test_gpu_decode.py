@@ -185,3 +185,27 @@ def test_decode_config4(dev, orc):
     stop = check_ids(list(ids), list(want_ids), want_logits)
     if stop is None:
         assert_close_f16(last_logits, want_logits[-1], what="step-32 logits")
+
+
+@pytest.mark.parametrize("dims", [
+    # (vocab, d, heads, layers, hidden, max_seq): head dims 16, 32, 64, 128,
+    # ragged column blocks (3d and hidden not multiples of 128)
+    [(512, 64, 4, 1, 96, 24), (1024, 256, 4, 2, 384, 40), (512, 64, 2, 2, 128, 16)],
+    [(256, 128, 1, 1, 200, 12), (520, 96, 2, 2, 136, 70), (256, 128, 1, 1, 200, 12)],
+])
+def test_decode_workspace_reuse(dev, orc, dims):
+    """Several model configurations in a row, smaller after larger: the
+    library's grow-only decode workspace and its counters are reused."""
+    import evk_amd as evk
+    for (vocab, d, heads, layers, hidden, max_seq) in dims:
+        kw = dict(vocab=vocab, d=d, heads=heads, layers=layers, hidden=hidden, max_seq=max_seq)
+        ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+        w = orc.model_weights(ocfg, seed=321 + d, std=0.1)
+        steps = 4
+        prompt = orc.tokens_u16(max_seq - steps - 1, 322 + d, vocab)
+        ids, first_logits, last_logits, _ = gpu_generate(evk, dev, cfg, w, prompt, steps)
+        want_ids, _, want_logits = orc.model_generate(ocfg, w, prompt, steps, return_logits=True)
+        assert_close_f16(first_logits, want_logits[0], what=f"prefill logits {kw}")
+        stop = check_ids(list(ids), list(want_ids), want_logits)
+        if stop is None:
+            assert_close_f16(last_logits, want_logits[-1], what=f"last logits {kw}")
