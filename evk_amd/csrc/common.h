@@ -92,6 +92,15 @@ DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
 DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+DEV float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+DEV float buf_load_f16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return (float)__builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0));
+}
+// An offset no descriptor covers (descriptors span < 2^31 bytes): a load at
+// it returns zeros, so predicated loads need no branch.
+DEV uint32_t oob_or(bool ok, uint32_t off) { return ok ? off : 0x80000000u; }
 
 DEV float wave_max(float v) {
 #pragma unroll

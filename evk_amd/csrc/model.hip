@@ -61,32 +61,32 @@ int gemv(const f16* x, const f16* W, f16* y, int K, int N, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // Fused decode step: five kernels per layer and one for the LM head.  Each
 // GEMV workgroup owns a 64-column block (one 128-byte line of every weight
-// row) over all K rows and runs its epilogue itself:
-//   qkv  : rms_norm(x) . Wqkv -> rope(q), rope(k), cache append (layer 0
-//          first takes x from the embedding row of the step's token)
-//   attn : single-query attention split over the cache, merged per head
-//   wo   : att . Wo, x += (residual)
-//   w1   : rms_norm(x) . W1 -> gelu
-//   w2   : gelu . W2, x += (residual)
-//   head : rms_norm(x) . Wout -> logits, greedy argmax (shader tie order)
-// Rounding points are those of the unfused op sequence (every op output is
-// fp16).  Partial sums are combined in a fixed order, so results do not
-// depend on which workgroup finishes last.
-// Cross-workgroup values are written and read with agent-scope atomics
-// (straight to the device coherence point, no L2 flush or invalidate), and
-// a workgroup counts itself in only after those stores have completed.
-// Counters are left at zero by the workgroup that consumes them.
+// row) over a K range and runs its prologue and epilogue itself:
+//   qkv  : x += pending W2 residual, rms_norm(x) . Wqkv -> rope(q), rope(k),
+//          cache append (layer 0 takes x from the embedding row instead)
+//   attn : single-query attention, each head split over key ranges
+//   wo   : merge of the attention splits, att . Wo over K ranges -> partials
+//   w1   : x += fp16(sum of the Wo partials), rms_norm(x) . W1 -> gelu
+//   w2   : gelu . W2 over K ranges -> partials (added by the next qkv/head)
+//   head : x += pending W2 residual, rms_norm(x) . Wout -> logits, greedy
+//          argmax (shader tie order)
+// Values cross workgroups only at kernel boundaries, except the LM head's
+// greedy winner.  Rounding points are those of the unfused op sequence
+// (every op output is fp16); partial sums are combined in a fixed order, so
+// results do not depend on which workgroup finishes last.
+// The LM head's block winners are written and read with agent-scope atomics
+// (straight to the device coherence point, no L2 flush or invalidate), and a
+// workgroup counts itself in only after those stores have completed; the
+// counter is left at zero by the workgroup that consumes it.
 // ---------------------------------------------------------------------------
 constexpr int GCB = 64;   // GEMV output columns per workgroup (128 bytes of a weight row)
-constexpr int ULD = 8;    // loads a thread keeps in flight
 
 struct DecArgs {
     int d, heads, dh, hidden, vocab, max_seq;
     float eps, rope_base;
-    f16* x;            // residual stream (d)
     f16* q;            // rope'd query (d)
-    f16* att;          // attention output (d)
     f16* hg;           // gelu(x . W1) (hidden)
+    float* apart;      // attention splits [split][head][dh + 4]: o / l, m, l
     float* cand_v;     // LM-head block winners
     uint32_t* cand_r;
     unsigned* cnt;     // counters (zero between launches)
@@ -110,42 +110,16 @@ DEV bool arrive_last(unsigned* cnt, unsigned total) {
     return s_last;
 }
 
-// sum_{k < n} p[k * stride], k ascending, with ULD loads in flight
-DEV float sum_strided_ag(const float* p, int n, int64_t stride) {
-    float s = 0.0f;
-    for (int k0 = 0; k0 < n; k0 += ULD) {
-        float v[ULD];
-#pragma unroll
-        for (int u = 0; u < ULD; ++u) v[u] = (k0 + u < n) ? ld_ag(p + (int64_t)(k0 + u) * stride) : 0.0f;
-#pragma unroll
-        for (int u = 0; u < ULD; ++u) s += v[u];
-    }
-    return s;
-}
-
-// Sum of squares of x (clamped to the fp16 range as rms_norm.comp does), in
-// the same order in every workgroup.
-template <int NT>
-DEV float block_sumsq(const f16* x, int d, float* red) {
-    float ss = 0.0f;
-    for (int j = threadIdx.x; j < d; j += NT) {
-        const float v = fminf(fmaxf((float)x[j], -65504.0f), 65504.0f);
-        ss += v * v;
-    }
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    ss = 0.0f;
-    for (int w = 0; w < NT / 64; ++w) ss += red[w];
-    __syncthreads();
-    return ss;
-}
-
-enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED_RMS = 2 };
-enum { EPI_QKV = 0, EPI_RESID = 1, EPI_GELU = 2, EPI_HEAD = 3 };
+enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED_RMS = 2, PRO_ATTN = 3 };
+enum { EPI_QKV = 0, EPI_PART = 1, EPI_GELU = 2, EPI_HEAD = 3 };
+constexpr int ATT_SMAX = 16;  // attention splits per head, at most
+constexpr int RES_SMAX = 8;   // K splits of a residual GEMV, at most
 
 struct GemvJob {
     const f16* in;    // input vector (PRO_PLAIN), or x (rms prologues)
+    const float* rpart;  // rms prologues: pending residual partials [rsplit][K]
+    int rsplit;
+    f16* xout;        // rms prologues: where workgroup (0, 0) stores the new x
     const f16* W;     // (K, N) row-major
     int K, N;
     // epilogue targets
@@ -156,18 +130,22 @@ struct GemvJob {
     const uint16_t* tok;
     f16* logits;      // EPI_HEAD
     uint16_t* out_id;
+    int nsplit;       // PRO_ATTN: attention splits per head
+    float* part;      // EPI_PART: K-split partials [ksplit][N]
 };
 
-// GEMV over all K rows of a block of NCB output columns (one 128-byte line of
+// GEMV over a K range of a block of NCB output columns (one 128-byte line of
 // each weight row when NCB = 64), with a prologue on the input vector and an
-// epilogue on the block's outputs in the same workgroup: no cross-workgroup
-// partials on the path.  NT threads = NCB/8 column groups x row groups; a
-// thread issues LD 16-byte weight loads before it waits, so that a block's
-// rows are in flight at once (256 threads x 24 loads cover K = 768).  Grid:
-// ceil(N / NCB); the input vector (K floats) lives in dynamic LDS.
+// epilogue on the block's outputs in the same workgroup.  Grid: (ceil(N /
+// NCB), ksplit); workgroup (cb, ks) takes rows [ks * kc, (ks + 1) * kc),
+// kc = ceil(K / ksplit).  NT threads = NCB/8 column groups x row groups; a
+// thread issues LD 16-byte weight loads before it waits, so that the range's
+// rows are in flight at once (256 threads x 24 loads cover 768 rows).  The
+// first batch is issued before the prologue: the weights do not depend on
+// the input vector, so both latencies overlap.  The input vector (K floats,
+// plus the staged attention splits for PRO_ATTN) lives in dynamic LDS.
 template <int NCB, int NT, int LD, int PRO, int EPI>
 __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
-    constexpr int GLD = LD;
     constexpr int CG = NCB / 8, RG = NT / CG;
     extern __shared__ float hv[];  // K input values
     __shared__ float red[RG * NCB];
@@ -176,51 +154,238 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     __shared__ uint32_t s_r[NT / 64];
     const int N = j.N, K = j.K;
     const int cb = blockIdx.x, c0 = cb * NCB, nc = min(NCB, N - c0);
+    const int kc = (K + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int r_lo = (int)blockIdx.y * kc, r_hi = min(K, r_lo + kc);
 
-    // The first batch of weight loads goes out before the prologue: the
-    // weights do not depend on the input vector, so both latencies overlap.
     const int cg = threadIdx.x % CG, rg = threadIdx.x / CG;
     const int col = c0 + cg * 8;
     const bool col_ok = col < N;
-    const f16* wp = j.W + col;
-    half8 w[GLD];
+    // loads are branch-free: offsets outside a descriptor read zeros
+    const __amdgpu_buffer_rsrc_t wres = buf_rsrc(j.W, (uint32_t)K * (uint32_t)N * 2u);
+    half8 w[LD];
     auto load_batch = [&](int i0) {
 #pragma unroll
-        for (int u = 0; u < GLD; ++u) {
+        for (int u = 0; u < LD; ++u) {
             const int i = i0 + u * RG;
-            w[u] = (col_ok && i < K) ? *reinterpret_cast<const half8*>(wp + (int64_t)i * N) : half8{};
+            w[u] = as_half8(buf_load16(wres, oob_or(col_ok && i < r_hi, ((uint32_t)i * (uint32_t)N + col) * 2u), 0));
         }
     };
-    load_batch(rg);
 
     // ---- prologue: the input vector as fp16 values ----
-    if (PRO == PRO_PLAIN) {
-        for (int i = threadIdx.x; i < K; i += NT) hv[i] = (float)j.in[i];
-    } else {
-        const f16* x = j.in;
-        if (PRO == PRO_EMBED_RMS) {
-            x = j.E + (int64_t)min((int)j.tok[0], a.vocab - 1) * K;
-            if (blockIdx.x == 0)
-                for (int t = threadIdx.x; t < K; t += NT) a.x[t] = x[t];
+    // For the sizes one pass of the workgroup covers (the "one" forms), the
+    // prologue's loads are issued first and the first batch of weight loads
+    // right after them (the weights do not depend on the input vector):
+    // loads complete in issue order, so the prologue then waits for its own
+    // data only, while the weights stream in.  The compiler barriers keep
+    // that issue order.
+    const int H = a.heads, dh = a.dh, W = dh + 4, S = j.nsplit;
+    const int h_lo = r_lo / dh, nh = (r_hi - 1) / dh - h_lo + 1;  // PRO_ATTN: heads of the range
+    const int per4 = nh * W / 4, tot4 = S * per4;                // PRO_ATTN: staged float4s
+    const f16* x = j.in;
+    if (PRO == PRO_EMBED_RMS) x = j.E + (int64_t)min((int)j.tok[0], a.vocab - 1) * K;
+    const int rs = (PRO == PRO_RMS) ? j.rsplit : 0;
+    const __amdgpu_buffer_rsrc_t xres = buf_rsrc(x, (uint32_t)K * 2u);
+    const __amdgpu_buffer_rsrc_t pres = buf_rsrc(j.rpart, (uint32_t)(rs * K) * 4u);  // splits >= rs read zeros
+    const __amdgpu_buffer_rsrc_t ares = buf_rsrc(a.apart, (uint32_t)(S * H * W) * 4u);
+    const bool one = (PRO == PRO_PLAIN)  ? (r_hi - r_lo <= 4 * NT)
+                     : (PRO == PRO_ATTN) ? (S > 1 && tot4 <= 8 * NT)
+                                         : (K <= 4 * NT);
+    uint32_t xv[4];  // raw fp16 bits
+    float pv[4][RES_SMAX];
+    u32x4 sv[8];
+    auto ld_h = [&](uint32_t off) { return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(xres, off, 0, 0); };
+    auto hval = [](uint32_t bits) { return (float)__builtin_bit_cast(f16, (uint16_t)bits); };
+    auto fetch_plain = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xv[u] = ld_h(oob_or(i0 + u * NT < r_hi, (uint32_t)(i0 + u * NT) * 2u));
+    };
+    auto fetch_stage = [&](int b0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int idx = b0 + u * NT, q = idx / per4;
+            const uint32_t off = (uint32_t)((q * H + h_lo) * (W / 4) + (idx - q * per4)) * 16u;
+            sv[u] = buf_load16(ares, oob_or(idx < tot4, off), 0);
         }
-        const float ss = block_sumsq<NT>(x, K, red);
+    };
+    auto fetch_x = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * NT;
+            xv[u] = ld_h(oob_or(i < K, (uint32_t)i * 2u));
+#pragma unroll
+            for (int q = 0; q < RES_SMAX; ++q) pv[u][q] = buf_load_f32(pres, oob_or(i < K, (uint32_t)(q * K + i) * 4u));
+        }
+    };
+    if (one) {
+        if (PRO == PRO_PLAIN) fetch_plain(r_lo + (int)threadIdx.x);
+        else if (PRO == PRO_ATTN) fetch_stage(threadIdx.x);
+        else fetch_x(threadIdx.x);
+    }
+    asm volatile("" ::: "memory");
+    load_batch(r_lo + rg);
+    asm volatile("" ::: "memory");
+    if (one) {  // the prologue's values are taken from here on
+        if (PRO == PRO_ATTN) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) asm volatile("" : "+v"(sv[u]));
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(xv[u]));
+            if (PRO == PRO_RMS) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int q = 0; q < RES_SMAX; ++q) asm volatile("" : "+v"(pv[u][q]));
+            }
+        }
+    }
+
+    if (PRO == PRO_PLAIN) {
+        auto put = [&](int i0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u * NT < r_hi) hv[i0 + u * NT] = hval(xv[u]);
+        };
+        if (one) {
+            put(r_lo + (int)threadIdx.x);
+        } else {
+            for (int i0 = r_lo + (int)threadIdx.x; i0 < r_hi; i0 += 4 * NT) {
+                fetch_plain(i0);
+                put(i0);
+            }
+        }
+    } else if (PRO == PRO_ATTN) {
+        // attention output of the heads in [r_lo, r_hi): each head's splits
+        // merged with weights l_s exp(m_s - M) / sum_s l_s exp(m_s - M); the
+        // splits of those heads are staged in LDS after hv as [split][head][W]
+        if (S == 1) {
+            for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += NT)
+                hv[i] = (float)(f16)a.apart[(i / dh) * W + i % dh];
+        } else {
+            float* stg = hv + K;
+            u32x4* dst = reinterpret_cast<u32x4*>(stg);
+            auto put = [&](int b0) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (b0 + u * NT < tot4) dst[b0 + u * NT] = sv[u];
+            };
+            if (one) {
+                put(threadIdx.x);
+            } else {
+                for (int b0 = threadIdx.x; b0 < tot4; b0 += 8 * NT) {
+                    fetch_stage(b0);
+                    put(b0);
+                }
+            }
+            __syncthreads();
+            auto head_weights = [&](int hh) {
+                float mv[ATT_SMAX], wv[ATT_SMAX];
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q) {
+                    const float* e = stg + (q * nh + hh) * W + dh;
+                    mv[q] = (q < S && e[1] > 0.0f) ? e[0] : -INFINITY;
+                    wv[q] = (q < S) ? e[1] : 0.0f;
+                }
+                float M = -INFINITY;
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q) M = fmaxf(M, mv[q]);
+                float den = 0.0f;
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q) {
+                    wv[q] = (mv[q] == -INFINITY) ? 0.0f : wv[q] * expf(mv[q] - M);
+                    den += wv[q];
+                }
+                const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q)
+                    if (q < S) stg[(q * nh + hh) * W + dh] = wv[q] * inv;
+            };
+            if (nh <= NT) {
+                if ((int)threadIdx.x < nh) head_weights(threadIdx.x);
+            } else {
+                for (int hh = threadIdx.x; hh < nh; hh += NT) head_weights(hh);
+            }
+            __syncthreads();
+            auto merge = [&](int i) {
+                const int hh = i / dh - h_lo, c = i % dh;
+                float wq[ATT_SMAX], oq[ATT_SMAX];
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q) {
+                    wq[q] = (q < S) ? stg[(q * nh + hh) * W + dh] : 0.0f;
+                    oq[q] = (q < S) ? stg[(q * nh + hh) * W + c] : 0.0f;
+                }
+                float v = 0.0f;
+#pragma unroll
+                for (int q = 0; q < ATT_SMAX; ++q) v += wq[q] * oq[q];
+                hv[i] = (float)(f16)v;
+            };
+            if (r_hi - r_lo <= NT) {
+                if (r_lo + (int)threadIdx.x < r_hi) merge(r_lo + threadIdx.x);
+            } else {
+                for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += NT) merge(i);
+            }
+        }
+    } else {
+        // x (or the embedding row of the step's token), plus the pending
+        // residual y = fp16(sum of the producer's K-split partials):
+        // x <- fp16(x + y).  Workgroup (0, 0) stores the new x to j.xout.
+        // Then rms_norm: fp16(clamp(x) / sqrt(mean(clamp(x)^2) + eps)).
+        const bool wr = j.xout != nullptr && blockIdx.x == 0 && blockIdx.y == 0;
+        float ss = 0.0f;
+        auto put = [&](int i0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * NT;
+                if (i >= K) continue;
+                float v = hval(xv[u]);
+                if (rs > 0) {
+                    float yv = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < RES_SMAX; ++q) yv += pv[u][q];
+                    v = (float)(f16)(v + (float)(f16)yv);
+                }
+                if (wr) j.xout[i] = (f16)v;
+                v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+                hv[i] = v;
+                ss += v * v;
+            }
+        };
+        if (one) {
+            put(threadIdx.x);
+        } else {
+            for (int i0 = threadIdx.x; i0 < K; i0 += 4 * NT) {
+                fetch_x(i0);
+                put(i0);
+            }
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < NT / 64; ++w2) ss += red[w2];
         const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
-        for (int i = threadIdx.x; i < K; i += NT) {
-            const float v = fminf(fmaxf((float)x[i], -65504.0f), 65504.0f);
-            hv[i] = (float)(f16)(v * inv);
+        if (one) {  // own elements
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = threadIdx.x + u * NT;
+                if (i < K) hv[i] = (float)(f16)(hv[i] * inv);
+            }
+        } else {
+            for (int i = threadIdx.x; i < K; i += NT) hv[i] = (float)(f16)(hv[i] * inv);
         }
     }
     __syncthreads();
 
-    // ---- the block's dot products ----
+    // ---- the block's dot products over rows [r_lo, r_hi) ----
     {
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int i0 = rg; i0 < K; i0 += RG * GLD) {
-            if (i0 != rg) load_batch(i0);
+        for (int i0 = r_lo + rg; i0 < r_hi; i0 += RG * LD) {
+            if (i0 != r_lo + rg) load_batch(i0);
 #pragma unroll
-            for (int u = 0; u < GLD; ++u) {
+            for (int u = 0; u < LD; ++u) {
                 const int i = i0 + u * RG;
-                const float h = (i < K) ? hv[i] : 0.0f;
+                const float h = (i < r_hi) ? hv[i] : 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[e] += h * (float)w[u][e];
             }
@@ -231,7 +396,7 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
         for (int c = threadIdx.x; c < NCB; c += NT) {
             float s = 0.0f;
             for (int r = 0; r < RG; ++r) s += red[r * NCB + c];
-            y[c] = (float)(f16)s;  // fp16 output of the product
+            y[c] = (EPI == EPI_PART) ? s : (float)(f16)s;  // fp16 output of the product, or a raw partial
         }
         __syncthreads();
     }
@@ -256,9 +421,9 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
             if (part == 0) a.q[jj] = r;
             else j.Kc[(int64_t)j.pos * d + jj] = r;
         }
-    } else if (EPI == EPI_RESID) {
-        for (int c = threadIdx.x; c < nc; c += NT)
-            a.x[c0 + c] = (f16)((float)a.x[c0 + c] + y[c]);
+    } else if (EPI == EPI_PART) {
+        float* out = j.part + (int64_t)blockIdx.y * N + c0;
+        for (int c = threadIdx.x; c < nc; c += NT) out[c] = y[c];
     } else if (EPI == EPI_GELU) {
         for (int c = threadIdx.x; c < nc; c += NT) a.hg[c0 + c] = (f16)gelu_f(y[c]);
     } else {  // EPI_HEAD: logits, then the greedy winner over all blocks
@@ -305,29 +470,31 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     }
 }
 
-// Single-query attention of one layer, one 1024-thread workgroup per head.
-// A pass covers ATT_KPT * 1024 / (dh / 16) keys; every K and V row of the
-// pass is requested before any arithmetic (a thread scores ATT_KPT keys with
-// dh / 16 lanes per key and sums 2 * ATT_KPT value rows of 8 dims), so the
-// head's cache arrives in one round trip per pass.  Scores, softmax and the
-// value sum stay in the workgroup; caches longer than a pass loop with an
-// online rescale.  Loads go through buffer descriptors over the valid rows
-// [0, L) with the whole offset in the range-checked vector operand, so rows
-// past the chain read as zeros.
-constexpr int ATT_NT = 1024;
-constexpr int ATT_KPT = 5;
+// Single-query attention of one layer: workgroup (h, s) covers keys
+// [s * ppw * kpp, +ppw * kpp) of head h, kpp = ATT_KPT * 256 / (dh / 16)
+// keys per pass.  Every K and V row of a pass is requested before any
+// arithmetic (a thread scores ATT_KPT keys with dh / 16 lanes per key and
+// sums 2 * ATT_KPT value rows of 8 dims), so a pass costs one round trip.
+// The split's result (o / l, m, l) goes to a.apart; the Wo GEMV merges the
+// splits in its prologue.  Loads go through buffer descriptors over the
+// valid rows [0, L) with the whole offset in the range-checked vector
+// operand: rows past the chain read as zeros, and keys past the split's
+// range are masked.
+constexpr int ATT_NT = 256;
+constexpr int ATT_KPT = 2;
 constexpr int ATT_VR = 2 * ATT_KPT;
 
-__global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, const f16* Vc, int L) {
+__global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, const f16* Vc, int L, int ppw) {
     __shared__ float sc[ATT_KPT * ATT_NT];
-    __shared__ float red[ATT_NT * 2];
+    __shared__ float red[ATT_NT * 8];
     __shared__ float stat[2 * (ATT_NT / 64)];
-    const int d = a.d, dh = a.dh, h = blockIdx.x;
+    const int d = a.d, dh = a.dh, h = blockIdx.x, sp = blockIdx.y;
     const float scale = 1.0f / sqrtf((float)dh);
     const int tpk = dh / 16, kstep = ATT_NT / tpk, kpp = ATT_KPT * kstep;
     const int ndg = dh / 8, G = ATT_NT / ndg;
     const int kl = threadIdx.x / tpk, part = threadIdx.x % tpk;
     const int dg = threadIdx.x % ndg, kg = threadIdx.x / ndg;
+    const int k_lo = sp * ppw * kpp, k_hi = min(L, k_lo + ppw * kpp);
     const uint32_t row = (uint32_t)d * 2;  // bytes per cache row
     const __amdgpu_buffer_rsrc_t kres = buf_rsrc(Kc, (uint32_t)L * row);
     const __amdgpu_buffer_rsrc_t vres = buf_rsrc(Vc, (uint32_t)L * row);
@@ -337,8 +504,8 @@ __global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, con
     const half8 q0 = qp[0], q1 = qp[1];
     float m_run = -INFINITY, l_run = 0.0f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < L; p0 += kpp) {
-        const int np = min(kpp, L - p0);
+    for (int p0 = k_lo; p0 < k_hi; p0 += kpp) {
+        const int np = min(kpp, k_hi - p0);
         half8 kv[ATT_KPT][2], v[ATT_VR];
 #pragma unroll
         for (int t = 0; t < ATT_KPT; ++t) {
@@ -396,26 +563,27 @@ __global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, con
         for (int e = 0; e < 8; ++e) o[e] *= alpha;
 #pragma unroll
         for (int u = 0; u < ATT_VR; ++u) {
-            const float pk = sc[kg + u * G];  // zero past np (rows read as zeros too)
+            const float pk = sc[kg + u * G];  // zero past np
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] += pk * (float)v[u][e];
         }
         __syncthreads();  // sc and stat are rewritten by the next pass
     }
-    // sum over the key groups: per dim group, G partial vectors of 8
-    // values, reduced through LDS in 4 rounds of a quarter of the threads
-    float tot = 0.0f;
-    const int dg2 = threadIdx.x / 8, e2 = threadIdx.x % 8;
-    for (int r = 0; r < 4; ++r) {
-        if (threadIdx.x / (ATT_NT / 4) == r)
+    // sum over the G key groups of each dim group
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red[(threadIdx.x % (ATT_NT / 4)) * 8 + e] = o[e];
-        __syncthreads();
-        if (threadIdx.x < dh)
-            for (int g = 0; g < G / 4; ++g) tot += red[(g * ndg + dg2) * 8 + e2];
-        __syncthreads();
+    for (int e = 0; e < 8; ++e) red[threadIdx.x * 8 + e] = o[e];
+    __syncthreads();
+    if (threadIdx.x < dh) {
+        const int dg2 = threadIdx.x / 8, e2 = threadIdx.x % 8;
+        float tot = 0.0f;
+        for (int g = 0; g < G; ++g) tot += red[(g * ndg + dg2) * 8 + e2];
+        float* out = a.apart + ((int64_t)sp * a.heads + h) * (dh + 4);
+        out[threadIdx.x] = l_run > 0.0f ? tot / l_run : 0.0f;
+        if (threadIdx.x == 0) {
+            out[dh] = m_run;
+            out[dh + 1] = l_run;
+        }
     }
-    if (threadIdx.x < dh) a.att[h * dh + threadIdx.x] = (f16)(l_run > 0.0f ? tot / l_run : 0.0f);
 }
 
 }  // namespace
@@ -453,30 +621,54 @@ uint64_t evkhip_model_cache_elems(const evkhip_model_cfg* c) {
 namespace evkhip {
 namespace {
 
-// Validates cfg/buffers and runs n tokens.  feed != null: token s is feed[s],
-// only the last step runs the LM head (into ids[0]); otherwise token s is
-// ids[s] and every step writes ids[s+1].
-// Rows in flight: 256 threads x 24 loads cover K <= 768 in one batch;
-// longer rows take 1024 threads x 12 loads per batch (K = 3072: two batches).
+// Rows in flight per workgroup: 256 threads hold 6, 12 or 24 loads of 32 row
+// groups (192, 384 or 768 rows per K range in one batch); longer ranges take
+// 1024 threads x 12 loads per batch.
+int gemv_rows_cap(int R) { return R <= 192 ? 192 : R <= 384 ? 384 : R <= 768 ? 768 : 0; }
+int gemv_static_lds(int R) { return gemv_rows_cap(R) ? 8448 : 33024; }
+
 template <int PRO, int EPI>
-void launch_gemv(dim3 grid, int K, const DecArgs& a, const GemvJob& j, hipStream_t st) {
-    const size_t lds = (size_t)K * sizeof(float);
-    if (K <= 24 * (256 / (GCB / 8)))
+void launch_gemv(int N, int K, int ksplit, size_t extra_lds, const DecArgs& a, const GemvJob& j, hipStream_t st) {
+    const dim3 grid((unsigned)((N + GCB - 1) / GCB), (unsigned)ksplit);
+    const size_t lds = (size_t)K * sizeof(float) + extra_lds;
+    const int cap = gemv_rows_cap((K + ksplit - 1) / ksplit);
+    if (cap == 192)
+        hipLaunchKernelGGL((dec_gemv<GCB, 256, 6, PRO, EPI>), grid, dim3(256), lds, st, a, j);
+    else if (cap == 384)
+        hipLaunchKernelGGL((dec_gemv<GCB, 256, 12, PRO, EPI>), grid, dim3(256), lds, st, a, j);
+    else if (cap == 768)
         hipLaunchKernelGGL((dec_gemv<GCB, 256, 24, PRO, EPI>), grid, dim3(256), lds, st, a, j);
     else
         hipLaunchKernelGGL((dec_gemv<GCB, 1024, 12, PRO, EPI>), grid, dim3(1024), lds, st, a, j);
 }
 
-// Fused path: five kernels per layer and one LM-head kernel per token.
+// K splits of the two residual GEMVs (Wo, W2): ranges of about 192 rows.
+int residual_ksplit(int K) { return std::min(RES_SMAX, (K + 191) / 192); }
+
+// Fused path: five kernels per layer and one LM-head kernel per token.  The
+// residual stream ping-pongs between two buffers: a kernel whose prologue
+// adds the pending residual reads x from one and workgroup (0, 0) stores the
+// sum to the other, which the following kernels read.
 int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, uint64_t per_layer, f16* cache_h,
                      const uint16_t* feed, uint16_t* ids, uint32_t n, uint32_t pos0, f16* logits, hipStream_t st) {
     const int d = (int)c.d, hid = (int)c.hidden, V = (int)c.vocab, H = (int)c.heads, dh = (int)c.dh;
     auto cdiv = [](int x, int y) { return (x + y - 1) / y; };
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int ks_o = residual_ksplit(d), ks_2 = residual_ksplit(hid);
+    // attention splits: as many as the Wo GEMV can stage in LDS next to its
+    // input vector, for the heads one K range of it covers
+    const int att_w = dh + 4;
+    const int ro = cdiv(d, ks_o);
+    const int nh_max = std::min(H, cdiv(ro, dh) + 1);
+    const int smax =
+        std::max(1, std::min(ATT_SMAX, (65536 - gemv_static_lds(ro) - d * 4) / (nh_max * att_w * 4)));
+    const int kpp = ATT_KPT * ATT_NT / (dh / 16);
     const size_t cnt_n = 1;  // the LM head's arrival counter
-    const size_t off_q = al((size_t)d * 2), off_att = off_q + al((size_t)d * 2);
-    const size_t off_hg = off_att + al((size_t)d * 2);
-    const size_t off_cv = off_hg + al((size_t)hid * 2);
+    const size_t off_xb = al((size_t)d * 2), off_q = off_xb + al((size_t)d * 2);
+    const size_t off_hg = off_q + al((size_t)d * 2);
+    const size_t off_apart = off_hg + al((size_t)hid * 2);
+    const size_t off_part = off_apart + al((size_t)smax * H * att_w * 4);
+    const size_t off_cv = off_part + al((size_t)RES_SMAX * d * 4);
     const size_t off_cr = off_cv + al((size_t)cdiv(V, GCB) * 4);
     const size_t need = off_cr + al((size_t)cdiv(V, GCB) * 4);
     if (need > g_fws.elems) {
@@ -498,14 +690,15 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
     DecArgs a{};
     a.d = d; a.heads = H; a.dh = dh; a.hidden = hid; a.vocab = V; a.max_seq = (int)c.max_seq;
     a.eps = c.eps; a.rope_base = c.rope_base;
-    a.x = reinterpret_cast<f16*>(base);
     a.q = reinterpret_cast<f16*>(base + off_q);
-    a.att = reinterpret_cast<f16*>(base + off_att);
     a.hg = reinterpret_cast<f16*>(base + off_hg);
+    a.apart = reinterpret_cast<float*>(base + off_apart);
     a.cand_v = reinterpret_cast<float*>(base + off_cv);
     a.cand_r = reinterpret_cast<uint32_t*>(base + off_cr);
     a.cnt = g_fcnt;
-    auto grid = [&](int N) { return dim3((unsigned)cdiv(N, GCB)); };
+    float* part = reinterpret_cast<float*>(base + off_part);
+    f16* xbuf[2] = {reinterpret_cast<f16*>(base), reinterpret_cast<f16*>(base + off_xb)};
+    int xc = 0;  // buffer holding x, up to the pending residual
     for (uint32_t s = 0; s < n; ++s) {
         const int pos = (int)(pos0 + s);
         const uint16_t* tok = feed ? feed + s : ids + s;
@@ -517,34 +710,50 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
             f16* Kc = cache_h + (uint64_t)l * 2 * c.max_seq * d;
             f16* Vc = Kc + (uint64_t)c.max_seq * d;
             GemvJob j{};
-            j.in = a.x; j.W = Wqkv; j.K = d; j.N = 3 * d; j.Kc = Kc; j.Vc = Vc; j.pos = pos; j.E = E; j.tok = tok;
-            if (l == 0)
-                launch_gemv<PRO_EMBED_RMS, EPI_QKV>(grid(3 * d), d, a, j, st);
-            else
-                launch_gemv<PRO_RMS, EPI_QKV>(grid(3 * d), d, a, j, st);
-            hipLaunchKernelGGL(dec_attn, dim3((unsigned)H), dim3(ATT_NT), 0, st, a, (const f16*)Kc, (const f16*)Vc,
-                               pos + 1);
+            j.W = Wqkv; j.K = d; j.N = 3 * d; j.Kc = Kc; j.Vc = Vc; j.pos = pos; j.E = E; j.tok = tok;
+            j.xout = xbuf[xc ^ 1];
+            if (l == 0) {
+                launch_gemv<PRO_EMBED_RMS, EPI_QKV>(3 * d, d, 1, 0, a, j, st);
+            } else {
+                j.in = xbuf[xc]; j.rpart = part; j.rsplit = ks_2;
+                launch_gemv<PRO_RMS, EPI_QKV>(3 * d, d, 1, 0, a, j, st);
+            }
+            xc ^= 1;
+            const int npass = cdiv(pos + 1, kpp);
+            const int ppw = cdiv(npass, std::min(npass, smax));
+            const int nsplit = cdiv(npass, ppw);  // every split holds at least one key
+            hipLaunchKernelGGL(dec_attn, dim3((unsigned)H, (unsigned)nsplit), dim3(ATT_NT), 0, st, a, (const f16*)Kc,
+                               (const f16*)Vc, pos + 1, ppw);
             GemvJob jo{};
-            jo.in = a.att; jo.W = Wo; jo.K = d; jo.N = d;
-            launch_gemv<PRO_PLAIN, EPI_RESID>(grid(d), d, a, jo, st);
+            jo.W = Wo; jo.K = d; jo.N = d; jo.nsplit = nsplit; jo.part = part;
+            const size_t stage = nsplit > 1 ? (size_t)nsplit * nh_max * att_w * 4 : 0;
+            launch_gemv<PRO_ATTN, EPI_PART>(d, d, ks_o, stage, a, jo, st);
             GemvJob j1{};
-            j1.in = a.x; j1.W = W1; j1.K = d; j1.N = hid;
-            launch_gemv<PRO_RMS, EPI_GELU>(grid(hid), d, a, j1, st);
+            j1.in = xbuf[xc]; j1.rpart = part; j1.rsplit = ks_o; j1.xout = xbuf[xc ^ 1];
+            j1.W = W1; j1.K = d; j1.N = hid;
+            launch_gemv<PRO_RMS, EPI_GELU>(hid, d, 1, 0, a, j1, st);
+            xc ^= 1;
             GemvJob j2{};
-            j2.in = a.hg; j2.W = W2; j2.K = hid; j2.N = d;
-            launch_gemv<PRO_PLAIN, EPI_RESID>(grid(d), hid, a, j2, st);
+            j2.in = a.hg; j2.W = W2; j2.K = hid; j2.N = d; j2.part = part;
+            launch_gemv<PRO_PLAIN, EPI_PART>(d, hid, ks_2, 0, a, j2, st);
         }
+        // x of the next step's layer 0 comes from the embedding; the last
+        // layer's W2 partials are still pending here
         if (!feed || s + 1 == n) {
             GemvJob jh{};
-            jh.in = a.x; jh.W = Wout; jh.K = d; jh.N = V; jh.logits = logits;
+            jh.in = xbuf[xc]; jh.rpart = part; jh.rsplit = ks_2;
+            jh.W = Wout; jh.K = d; jh.N = V; jh.logits = logits;
             jh.out_id = feed ? ids : ids + s + 1;
-            launch_gemv<PRO_RMS, EPI_HEAD>(grid(V), d, a, jh, st);
+            launch_gemv<PRO_RMS, EPI_HEAD>(V, d, 1, 0, a, jh, st);
         }
     }
     EVK_HIP(hipGetLastError());
     return EVKHIP_OK;
 }
 
+// Validates cfg/buffers and runs n tokens.  feed != null: token s is feed[s],
+// only the last step runs the LM head (into ids[0]); otherwise token s is
+// ids[s] and every step writes ids[s+1].
 int run_tokens(const evkhip_model_cfg* cfg, const void* weights, void* cache, const uint16_t* feed,
                uint16_t* ids, uint32_t n, uint32_t pos0, void* logits, hipStream_t st) {
     EVK_RETURN_IF(!cfg || !weights || !cache || !ids || !logits, EVKHIP_ERR_INVALID_ARG,
@@ -588,7 +797,8 @@ int run_tokens(const evkhip_model_cfg* cfg, const void* weights, void* cache, co
     // (the fused GEMVs keep their input vector in LDS: K floats next to 33 KB
     // of reduction space, within 64 KB per workgroup)
     if ((c.dh == 16 || c.dh == 32 || c.dh == 64 || c.dh == 128) && c.d <= 7680 && c.hidden <= 7680 &&
-        (int64_t)c.max_seq * c.d * 2 < INT32_MAX)
+        (int64_t)c.max_seq * c.d * 2 < INT32_MAX && (int64_t)c.vocab * c.d * 2 < INT32_MAX &&
+        (int64_t)c.hidden * c.d * 2 < INT32_MAX)
         return run_tokens_fused(c, W.E, W.Wout, W.per_layer, cache_h, feed, ids, n, pos0, (f16*)logits, st);
 
     for (uint32_t s = 0; s < n; ++s) {
