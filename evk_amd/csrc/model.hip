@@ -84,8 +84,6 @@ constexpr int GCB = 64;   // GEMV output columns per workgroup (128 bytes of a w
 struct DecArgs {
     int d, heads, dh, hidden, vocab, max_seq;
     float eps, rope_base;
-    f16* q;            // rope'd query (d)
-    f16* hg;           // gelu(x . W1) (hidden)
     float* apart;      // attention splits [split][head][dh + 4]: o / l, m, l
     float* cand_v;     // LM-head block winners
     uint32_t* cand_r;
@@ -110,22 +108,18 @@ DEV bool arrive_last(unsigned* cnt, unsigned total) {
     return s_last;
 }
 
-enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED_RMS = 2, PRO_ATTN = 3 };
-enum { EPI_QKV = 0, EPI_PART = 1, EPI_GELU = 2, EPI_HEAD = 3 };
+enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED_RMS = 2, PRO_ATTN = 3, PRO_GELU = 4 };
+enum { EPI_PART = 0, EPI_HEAD = 1 };
 constexpr int ATT_SMAX = 16;  // attention splits per head, at most
 constexpr int RES_SMAX = 8;   // K splits of a residual GEMV, at most
 
 struct GemvJob {
     const f16* in;    // input vector (PRO_PLAIN), or x (rms prologues)
-    const float* rpart;  // rms prologues: pending residual partials [rsplit][K]
+    const float* rpart;  // rms / gelu prologues: the producer's partials [rsplit][K]
     int rsplit;
     f16* xout;        // rms prologues: where workgroup (0, 0) stores the new x
     const f16* W;     // (K, N) row-major
     int K, N;
-    // epilogue targets
-    f16* Kc;          // EPI_QKV: this layer's caches
-    f16* Vc;
-    int pos;
     const f16* E;     // PRO_EMBED_RMS: embedding table and the step's token
     const uint16_t* tok;
     f16* logits;      // EPI_HEAD
@@ -183,11 +177,11 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     const int per4 = nh * W / 4, tot4 = S * per4;                // PRO_ATTN: staged float4s
     const f16* x = j.in;
     if (PRO == PRO_EMBED_RMS) x = j.E + (int64_t)min((int)j.tok[0], a.vocab - 1) * K;
-    const int rs = (PRO == PRO_RMS) ? j.rsplit : 0;
+    const int rs = (PRO == PRO_RMS || PRO == PRO_GELU) ? j.rsplit : 0;
     const __amdgpu_buffer_rsrc_t xres = buf_rsrc(x, (uint32_t)K * 2u);
     const __amdgpu_buffer_rsrc_t pres = buf_rsrc(j.rpart, (uint32_t)(rs * K) * 4u);  // splits >= rs read zeros
     const __amdgpu_buffer_rsrc_t ares = buf_rsrc(a.apart, (uint32_t)(S * H * W) * 4u);
-    const bool one = (PRO == PRO_PLAIN)  ? (r_hi - r_lo <= 4 * NT)
+    const bool one = (PRO == PRO_PLAIN || PRO == PRO_GELU) ? (r_hi - r_lo <= 4 * NT)
                      : (PRO == PRO_ATTN) ? (S > 1 && tot4 <= 8 * NT)
                                          : (K <= 4 * NT);
     uint32_t xv[4];  // raw fp16 bits
@@ -207,6 +201,15 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
             sv[u] = buf_load16(ares, oob_or(idx < tot4, off), 0);
         }
     };
+    auto fetch_gelu = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * NT;
+#pragma unroll
+            for (int q = 0; q < RES_SMAX; ++q)
+                pv[u][q] = buf_load_f32(pres, oob_or(i < r_hi, (uint32_t)(q * K + i) * 4u));
+        }
+    };
     auto fetch_x = [&](int i0) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -218,6 +221,7 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     };
     if (one) {
         if (PRO == PRO_PLAIN) fetch_plain(r_lo + (int)threadIdx.x);
+        else if (PRO == PRO_GELU) fetch_gelu(r_lo + (int)threadIdx.x);
         else if (PRO == PRO_ATTN) fetch_stage(threadIdx.x);
         else fetch_x(threadIdx.x);
     }
@@ -229,9 +233,11 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) asm volatile("" : "+v"(sv[u]));
         } else {
+            if (PRO != PRO_GELU) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(xv[u]));
-            if (PRO == PRO_RMS) {
+                for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(xv[u]));
+            }
+            if (PRO == PRO_RMS || PRO == PRO_GELU) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -254,10 +260,32 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
                 put(i0);
             }
         }
+    } else if (PRO == PRO_GELU) {
+        // gelu(fp16(sum of the W1 partials)) of the rows [r_lo, r_hi)
+        auto put = [&](int i0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * NT;
+                if (i >= r_hi) continue;
+                float yv = 0.0f;
+#pragma unroll
+                for (int q = 0; q < RES_SMAX; ++q) yv += pv[u][q];
+                hv[i] = (float)(f16)gelu_f((float)(f16)yv);
+            }
+        };
+        if (one) {
+            put(r_lo + (int)threadIdx.x);
+        } else {
+            for (int i0 = r_lo + (int)threadIdx.x; i0 < r_hi; i0 += 4 * NT) {
+                fetch_gelu(i0);
+                put(i0);
+            }
+        }
     } else if (PRO == PRO_ATTN) {
         // attention output of the heads in [r_lo, r_hi): each head's splits
-        // merged with weights l_s exp(m_s - M) / sum_s l_s exp(m_s - M); the
-        // splits of those heads are staged in LDS after hv as [split][head][W]
+        // (o_s / l_s, m_s, l_s) merged as sum_s w_s o_s / l_s / sum_s w_s with
+        // w_s = l_s exp(m_s - max m); the splits of those heads are staged in
+        // LDS after hv as [split][head][W]
         if (S == 1) {
             for (int i = r_lo + (int)threadIdx.x; i < r_hi; i += NT)
                 hv[i] = (float)(f16)a.apart[(i / dh) * W + i % dh];
@@ -278,46 +306,28 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
                 }
             }
             __syncthreads();
-            auto head_weights = [&](int hh) {
-                float mv[ATT_SMAX], wv[ATT_SMAX];
+            auto merge = [&](int i) {
+                const int hh = i / dh - h_lo, c = i % dh;
+                float mq[ATT_SMAX], lq[ATT_SMAX], oq[ATT_SMAX];
 #pragma unroll
                 for (int q = 0; q < ATT_SMAX; ++q) {
-                    const float* e = stg + (q * nh + hh) * W + dh;
-                    mv[q] = (q < S && e[1] > 0.0f) ? e[0] : -INFINITY;
-                    wv[q] = (q < S) ? e[1] : 0.0f;
+                    const float* e = stg + (q * nh + hh) * W;
+                    lq[q] = (q < S) ? e[dh + 1] : 0.0f;
+                    mq[q] = (q < S) ? e[dh] : -INFINITY;
+                    oq[q] = (q < S) ? e[c] : 0.0f;
                 }
                 float M = -INFINITY;
 #pragma unroll
-                for (int q = 0; q < ATT_SMAX; ++q) M = fmaxf(M, mv[q]);
-                float den = 0.0f;
-#pragma unroll
-                for (int q = 0; q < ATT_SMAX; ++q) {
-                    wv[q] = (mv[q] == -INFINITY) ? 0.0f : wv[q] * expf(mv[q] - M);
-                    den += wv[q];
-                }
-                const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-#pragma unroll
                 for (int q = 0; q < ATT_SMAX; ++q)
-                    if (q < S) stg[(q * nh + hh) * W + dh] = wv[q] * inv;
-            };
-            if (nh <= NT) {
-                if ((int)threadIdx.x < nh) head_weights(threadIdx.x);
-            } else {
-                for (int hh = threadIdx.x; hh < nh; hh += NT) head_weights(hh);
-            }
-            __syncthreads();
-            auto merge = [&](int i) {
-                const int hh = i / dh - h_lo, c = i % dh;
-                float wq[ATT_SMAX], oq[ATT_SMAX];
+                    if (lq[q] > 0.0f) M = fmaxf(M, mq[q]);
+                float num = 0.0f, den = 0.0f;
 #pragma unroll
                 for (int q = 0; q < ATT_SMAX; ++q) {
-                    wq[q] = (q < S) ? stg[(q * nh + hh) * W + dh] : 0.0f;
-                    oq[q] = (q < S) ? stg[(q * nh + hh) * W + c] : 0.0f;
+                    const float wq = (lq[q] > 0.0f) ? lq[q] * expf(mq[q] - M) : 0.0f;
+                    num += wq * oq[q];
+                    den += wq;
                 }
-                float v = 0.0f;
-#pragma unroll
-                for (int q = 0; q < ATT_SMAX; ++q) v += wq[q] * oq[q];
-                hv[i] = (float)(f16)v;
+                hv[i] = (float)(f16)(den > 0.0f ? num / den : 0.0f);
             };
             if (r_hi - r_lo <= NT) {
                 if (r_lo + (int)threadIdx.x < r_hi) merge(r_lo + threadIdx.x);
@@ -402,30 +412,9 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     }
 
     // ---- epilogue ----
-    if (EPI == EPI_QKV) {
-        const int d = a.d;
-        for (int c = threadIdx.x; c < nc; c += NT) {
-            const int col = c0 + c;
-            const int part = col / d, jj = col % d;
-            if (part == 2) {
-                j.Vc[(int64_t)j.pos * d + jj] = (f16)y[c];
-                continue;
-            }
-            const float x0 = y[c & ~1], x1 = y[c | 1];
-            const int pp = (jj % a.dh) / 2;
-            const float inv_freq = powf(a.rope_base, -2.0f * (float)pp / (float)a.dh);
-            const float ang = (float)j.pos * inv_freq;
-            float sn, cs;
-            sincosf(ang, &sn, &cs);
-            const f16 r = (f16)((c & 1) ? (x0 * sn + x1 * cs) : (x0 * cs - x1 * sn));
-            if (part == 0) a.q[jj] = r;
-            else j.Kc[(int64_t)j.pos * d + jj] = r;
-        }
-    } else if (EPI == EPI_PART) {
+    if (EPI == EPI_PART) {
         float* out = j.part + (int64_t)blockIdx.y * N + c0;
         for (int c = threadIdx.x; c < nc; c += NT) out[c] = y[c];
-    } else if (EPI == EPI_GELU) {
-        for (int c = threadIdx.x; c < nc; c += NT) a.hg[c0 + c] = (f16)gelu_f(y[c]);
     } else {  // EPI_HEAD: logits, then the greedy winner over all blocks
         const int ncb = (N + NCB - 1) / NCB;
         float bv = -3.402823466e+38f;
@@ -470,25 +459,35 @@ __global__ __launch_bounds__(NT) void dec_gemv(DecArgs a, GemvJob j) {
     }
 }
 
-// Single-query attention of one layer: workgroup (h, s) covers keys
-// [s * ppw * kpp, +ppw * kpp) of head h, kpp = ATT_KPT * 256 / (dh / 16)
-// keys per pass.  Every K and V row of a pass is requested before any
-// arithmetic (a thread scores ATT_KPT keys with dh / 16 lanes per key and
-// sums 2 * ATT_KPT value rows of 8 dims), so a pass costs one round trip.
-// The split's result (o / l, m, l) goes to a.apart; the Wo GEMV merges the
-// splits in its prologue.  Loads go through buffer descriptors over the
-// valid rows [0, L) with the whole offset in the range-checked vector
-// operand: rows past the chain read as zeros, and keys past the split's
-// range are masked.
+// Single-query attention of one layer, with the QKV GEMV's K-split
+// partials merged in its prologue: workgroup (h, s) forms q of head h
+// (fp16(sum of partials), rope, fp16) and covers the cached keys
+// [s * ppw * kpp, +ppw * kpp) below pos, kpp = ATT_KPT * 256 / (dh / 16)
+// keys per pass.  The last split also forms k, v of position pos (rope on
+// k), appends them to the caches and folds that key in after its range.
+// Every K and V row of a pass is requested before any arithmetic (a thread
+// scores ATT_KPT keys with dh / 16 lanes per key and sums 2 * ATT_KPT value
+// rows of 8 dims), so a pass costs one round trip; the first pass is
+// requested together with the partials.  The split's result (o / l, m, l)
+// goes to a.apart; the Wo GEMV merges the splits in its prologue.  Loads go
+// through buffer descriptors over the cached rows [0, pos) with the whole
+// offset in the range-checked vector operand: rows past them read as
+// zeros, and keys past the split's range are masked.
 constexpr int ATT_NT = 256;
 constexpr int ATT_KPT = 2;
 constexpr int ATT_VR = 2 * ATT_KPT;
 
-__global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, const f16* Vc, int L, int ppw) {
+__global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, f16* Kc, f16* Vc, const float* qkv_part, int qsplit,
+                                                   int pos, int ppw) {
     __shared__ float sc[ATT_KPT * ATT_NT];
     __shared__ float red[ATT_NT * 8];
     __shared__ float stat[2 * (ATT_NT / 64)];
+    __shared__ float pre[3 * 128];            // fp16-rounded sums of q, k, v of the head
+    __shared__ __attribute__((aligned(16))) f16 qh[128];
+    __shared__ float kvn[2 * 128];            // k (rope'd), v of position pos
     const int d = a.d, dh = a.dh, h = blockIdx.x, sp = blockIdx.y;
+    const bool last = sp + 1 == (int)gridDim.y;
+    const int L = pos;  // cached keys
     const float scale = 1.0f / sqrtf((float)dh);
     const int tpk = dh / 16, kstep = ATT_NT / tpk, kpp = ATT_KPT * kstep;
     const int ndg = dh / 8, G = ATT_NT / ndg;
@@ -500,13 +499,24 @@ __global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, con
     const __amdgpu_buffer_rsrc_t vres = buf_rsrc(Vc, (uint32_t)L * row);
     const uint32_t kvo = (uint32_t)kl * row + (uint32_t)(h * dh + part * 16) * 2;
     const uint32_t vvo = (uint32_t)kg * row + (uint32_t)(h * dh + dg * 8) * 2;
-    const half8* qp = reinterpret_cast<const half8*>(a.q + h * dh + part * 16);
-    const half8 q0 = qp[0], q1 = qp[1];
-    float m_run = -INFINITY, l_run = 0.0f;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p0 = k_lo; p0 < k_hi; p0 += kpp) {
-        const int np = min(kpp, k_hi - p0);
-        half8 kv[ATT_KPT][2], v[ATT_VR];
+
+    // partials of q (and k, v for the last split): entry t < dh (or < 3 dh),
+    // t = threadIdx.x + u * ATT_NT, sums column (t / dh) * d + h * dh + t % dh
+    // over the splits
+    const int nsum = last ? 3 * dh : dh;
+    const __amdgpu_buffer_rsrc_t pres = buf_rsrc(qkv_part, (uint32_t)(qsplit * 3 * d) * 4u);  // splits >= qsplit: zeros
+    float pv[2][RES_SMAX];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t = threadIdx.x + u * ATT_NT;
+        const int pc = (t / dh) * d + h * dh + t % dh;
+#pragma unroll
+        for (int q = 0; q < RES_SMAX; ++q) pv[u][q] = buf_load_f32(pres, oob_or(t < nsum, (uint32_t)(q * 3 * d + pc) * 4u));
+    }
+    asm volatile("" ::: "memory");
+
+    half8 kv[ATT_KPT][2], v[ATT_VR];
+    auto load_pass = [&](int p0) {
 #pragma unroll
         for (int t = 0; t < ATT_KPT; ++t) {
             const uint32_t vo = kvo + (uint32_t)(p0 + t * kstep) * row;
@@ -515,6 +525,53 @@ __global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, con
         }
 #pragma unroll
         for (int u = 0; u < ATT_VR; ++u) v[u] = as_half8(buf_load16(vres, vvo + (uint32_t)(p0 + u * G) * row, 0));
+    };
+    if (k_lo < k_hi) load_pass(k_lo);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int q = 0; q < RES_SMAX; ++q) asm volatile("" : "+v"(pv[u][q]));
+
+    // q, k, v of the head: fp16 sums, then rope on q and k (pairs 2i, 2i+1)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int t = threadIdx.x + u * ATT_NT;
+        float y = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RES_SMAX; ++q) y += pv[u][q];
+        if (t < nsum) pre[t] = (float)(f16)y;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < nsum; t += ATT_NT) {
+        const int which = t / dh, c = t % dh;
+        if (which == 2) {
+            const float vn = pre[t];
+            kvn[dh + c] = vn;
+            Vc[(int64_t)pos * d + h * dh + c] = (f16)vn;
+        } else {
+            const float x0 = pre[which * dh + (c & ~1)], x1 = pre[which * dh + (c | 1)];
+            const float inv_freq = powf(a.rope_base, -2.0f * (float)(c / 2) / (float)dh);
+            float sn, cs;
+            sincosf((float)pos * inv_freq, &sn, &cs);
+            const f16 r = (f16)((c & 1) ? (x0 * sn + x1 * cs) : (x0 * cs - x1 * sn));
+            if (which == 0) {
+                qh[c] = r;
+            } else {
+                kvn[c] = (float)r;
+                Kc[(int64_t)pos * d + h * dh + c] = r;
+            }
+        }
+    }
+    __syncthreads();
+    const half8 q0 = *reinterpret_cast<const half8*>(qh + part * 16);
+    const half8 q1 = *reinterpret_cast<const half8*>(qh + part * 16 + 8);
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p0 = k_lo; p0 < k_hi; p0 += kpp) {
+        const int np = min(kpp, k_hi - p0);
+        if (p0 != k_lo) load_pass(p0);
         // scores
         float mx = -INFINITY;
 #pragma unroll
@@ -572,11 +629,27 @@ __global__ __launch_bounds__(ATT_NT) void dec_attn(DecArgs a, const f16* Kc, con
     // sum over the G key groups of each dim group
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[threadIdx.x * 8 + e] = o[e];
+    // the last split's new key: score q . k, summed by wave 0
+    if (last && threadIdx.x < 64) {
+        float sn = 0.0f;
+        for (int c = threadIdx.x; c < dh; c += 64) sn += (float)qh[c] * kvn[c];
+        sn = wave_sum(sn);
+        if (threadIdx.x == 0) stat[0] = sn * scale;
+    }
     __syncthreads();
+    const float s_new = stat[0];
     if (threadIdx.x < dh) {
         const int dg2 = threadIdx.x / 8, e2 = threadIdx.x % 8;
         float tot = 0.0f;
         for (int g = 0; g < G; ++g) tot += red[(g * ndg + dg2) * 8 + e2];
+        if (last) {
+            const float m_new = fmaxf(m_run, s_new);
+            const float alpha = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
+            const float pn = expf(s_new - m_new);
+            tot = tot * alpha + pn * kvn[dh + threadIdx.x];
+            l_run = l_run * alpha + pn;
+            m_run = m_new;
+        }
         float* out = a.apart + ((int64_t)sp * a.heads + h) * (dh + 4);
         out[threadIdx.x] = l_run > 0.0f ? tot / l_run : 0.0f;
         if (threadIdx.x == 0) {
@@ -664,11 +737,12 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
         std::max(1, std::min(ATT_SMAX, (65536 - gemv_static_lds(ro) - d * 4) / (nh_max * att_w * 4)));
     const int kpp = ATT_KPT * ATT_NT / (dh / 16);
     const size_t cnt_n = 1;  // the LM head's arrival counter
-    const size_t off_xb = al((size_t)d * 2), off_q = off_xb + al((size_t)d * 2);
-    const size_t off_hg = off_q + al((size_t)d * 2);
-    const size_t off_apart = off_hg + al((size_t)hid * 2);
-    const size_t off_part = off_apart + al((size_t)smax * H * att_w * 4);
-    const size_t off_cv = off_part + al((size_t)RES_SMAX * d * 4);
+    const int ks_q = residual_ksplit(d), ks_1 = residual_ksplit(d);
+    const size_t part_n = (size_t)RES_SMAX * std::max(3 * d, hid);
+    const size_t off_xb = al((size_t)d * 2);
+    const size_t off_pa = off_xb + al((size_t)d * 2), off_pb = off_pa + al(part_n * 4);
+    const size_t off_apart = off_pb + al(part_n * 4);
+    const size_t off_cv = off_apart + al((size_t)smax * H * att_w * 4);
     const size_t off_cr = off_cv + al((size_t)cdiv(V, GCB) * 4);
     const size_t need = off_cr + al((size_t)cdiv(V, GCB) * 4);
     if (need > g_fws.elems) {
@@ -690,13 +764,14 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
     DecArgs a{};
     a.d = d; a.heads = H; a.dh = dh; a.hidden = hid; a.vocab = V; a.max_seq = (int)c.max_seq;
     a.eps = c.eps; a.rope_base = c.rope_base;
-    a.q = reinterpret_cast<f16*>(base + off_q);
-    a.hg = reinterpret_cast<f16*>(base + off_hg);
     a.apart = reinterpret_cast<float*>(base + off_apart);
     a.cand_v = reinterpret_cast<float*>(base + off_cv);
     a.cand_r = reinterpret_cast<uint32_t*>(base + off_cr);
     a.cnt = g_fcnt;
-    float* part = reinterpret_cast<float*>(base + off_part);
+    // partials: QKV and W1 write A, Wo and W2 write B; every kernel reads
+    // the other buffer than the one it writes
+    float* pa = reinterpret_cast<float*>(base + off_pa);
+    float* pb = reinterpret_cast<float*>(base + off_pb);
     f16* xbuf[2] = {reinterpret_cast<f16*>(base), reinterpret_cast<f16*>(base + off_xb)};
     int xc = 0;  // buffer holding x, up to the pending residual
     for (uint32_t s = 0; s < n; ++s) {
@@ -710,38 +785,38 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
             f16* Kc = cache_h + (uint64_t)l * 2 * c.max_seq * d;
             f16* Vc = Kc + (uint64_t)c.max_seq * d;
             GemvJob j{};
-            j.W = Wqkv; j.K = d; j.N = 3 * d; j.Kc = Kc; j.Vc = Vc; j.pos = pos; j.E = E; j.tok = tok;
+            j.W = Wqkv; j.K = d; j.N = 3 * d; j.E = E; j.tok = tok; j.part = pa;
             j.xout = xbuf[xc ^ 1];
             if (l == 0) {
-                launch_gemv<PRO_EMBED_RMS, EPI_QKV>(3 * d, d, 1, 0, a, j, st);
+                launch_gemv<PRO_EMBED_RMS, EPI_PART>(3 * d, d, ks_q, 0, a, j, st);
             } else {
-                j.in = xbuf[xc]; j.rpart = part; j.rsplit = ks_2;
-                launch_gemv<PRO_RMS, EPI_QKV>(3 * d, d, 1, 0, a, j, st);
+                j.in = xbuf[xc]; j.rpart = pb; j.rsplit = ks_2;
+                launch_gemv<PRO_RMS, EPI_PART>(3 * d, d, ks_q, 0, a, j, st);
             }
             xc ^= 1;
-            const int npass = cdiv(pos + 1, kpp);
+            const int npass = std::max(1, cdiv(pos, kpp));
             const int ppw = cdiv(npass, std::min(npass, smax));
-            const int nsplit = cdiv(npass, ppw);  // every split holds at least one key
-            hipLaunchKernelGGL(dec_attn, dim3((unsigned)H, (unsigned)nsplit), dim3(ATT_NT), 0, st, a, (const f16*)Kc,
-                               (const f16*)Vc, pos + 1, ppw);
+            const int nsplit = cdiv(npass, ppw);  // the last split also takes key pos
+            hipLaunchKernelGGL(dec_attn, dim3((unsigned)H, (unsigned)nsplit), dim3(ATT_NT), 0, st, a, Kc, Vc,
+                               (const float*)pa, ks_q, pos, ppw);
             GemvJob jo{};
-            jo.W = Wo; jo.K = d; jo.N = d; jo.nsplit = nsplit; jo.part = part;
+            jo.W = Wo; jo.K = d; jo.N = d; jo.nsplit = nsplit; jo.part = pb;
             const size_t stage = nsplit > 1 ? (size_t)nsplit * nh_max * att_w * 4 : 0;
             launch_gemv<PRO_ATTN, EPI_PART>(d, d, ks_o, stage, a, jo, st);
             GemvJob j1{};
-            j1.in = xbuf[xc]; j1.rpart = part; j1.rsplit = ks_o; j1.xout = xbuf[xc ^ 1];
-            j1.W = W1; j1.K = d; j1.N = hid;
-            launch_gemv<PRO_RMS, EPI_GELU>(hid, d, 1, 0, a, j1, st);
+            j1.in = xbuf[xc]; j1.rpart = pb; j1.rsplit = ks_o; j1.xout = xbuf[xc ^ 1];
+            j1.W = W1; j1.K = d; j1.N = hid; j1.part = pa;
+            launch_gemv<PRO_RMS, EPI_PART>(hid, d, ks_1, 0, a, j1, st);
             xc ^= 1;
             GemvJob j2{};
-            j2.in = a.hg; j2.W = W2; j2.K = hid; j2.N = d; j2.part = part;
-            launch_gemv<PRO_PLAIN, EPI_PART>(d, hid, ks_2, 0, a, j2, st);
+            j2.rpart = pa; j2.rsplit = ks_1; j2.W = W2; j2.K = hid; j2.N = d; j2.part = pb;
+            launch_gemv<PRO_GELU, EPI_PART>(d, hid, ks_2, 0, a, j2, st);
         }
         // x of the next step's layer 0 comes from the embedding; the last
         // layer's W2 partials are still pending here
         if (!feed || s + 1 == n) {
             GemvJob jh{};
-            jh.in = xbuf[xc]; jh.rpart = part; jh.rsplit = ks_2;
+            jh.in = xbuf[xc]; jh.rpart = pb; jh.rsplit = ks_2;
             jh.W = Wout; jh.K = d; jh.N = V; jh.logits = logits;
             jh.out_id = feed ? ids : ids + s + 1;
             launch_gemv<PRO_RMS, EPI_HEAD>(V, d, 1, 0, a, jh, st);
