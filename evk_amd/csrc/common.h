@@ -84,6 +84,24 @@ DEV void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
     }
 }
 
+DEV floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 over a row-major 16-bit LDS tile: in each group of 16
+// lanes, lane i passes the address of row i / 4, columns 4 (i % 4) .. +3 of a
+// 4-row x 16-column block and receives column i of the block (its 4 rows).
+DEV half4 lds_read_tr(const f16* p) {
+    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (__attribute__((address_space(3))) fp16x4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+DEV half8 cat4(const half4& a, const half4& b) {
+    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 // Raw buffer loads: a descriptor over [base, base + bytes); a 16-byte load
 // at byte offset voff + soff past the end returns zeros.
 DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {

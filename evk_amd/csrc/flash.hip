@@ -143,22 +143,6 @@ DEV half8 pack8v(const floatx16& x, int off) {
 constexpr int FR = 64;  // query rows per workgroup (4 waves x 16)
 constexpr int KT = 64;  // keys per LDS tile
 
-DEV floatx4 mfma16(const half8& a, const half8& b, const floatx4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
-// 4 consecutive rows of one column of a row-major 16-bit LDS tile
-// (ds_read_b64_tr_b16); `p` is this lane's address as described above.
-DEV half4 lds_read_tr(const f16* p) {
-    fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-        (__attribute__((address_space(3))) fp16x4_t*)(p));
-    return __builtin_bit_cast(half4, v);
-}
-
-DEV half8 cat4(const half4& a, const half4& b) {
-    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
 
 DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

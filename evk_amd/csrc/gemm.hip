@@ -17,6 +17,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <utility>
 
 namespace evkhip {
 
@@ -206,6 +207,232 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled(GemmArgs p) {
         }
 }
 
+// ---- MFMA kernel: BM x BN tiles, 4 waves of (BM/2) x (BN/2) ---------------
+// v_mfma_f32_16x16x32_f16 (lane l: A row l%16 / B column l%16, k 8(l/16)..+8;
+// D column l%16, rows 4(l/16)..+3).  Each operand tile of BK = 64 along K
+// goes from global memory straight into LDS (buffer_load_dwordx4 ... lds: a
+// wave instruction fills 1 KB, lane i the 16 bytes at i*16) as it lies in
+// memory, with the 16-byte chunks of a row permuted so that the fragment
+// reads hit distinct banks:
+//   k-contiguous operand (A row-major, B stored (N,K)): rows of 64 halves,
+//     chunk c of row r at slot c ^ (r & 7); fragments by ds_read_b128.
+//   m/n-contiguous operand (A stored (K,M), B row-major): rows of BM / BN
+//     halves, chunk c of row r at slot c ^ 2 (r & 3); fragments by
+//     ds_read_b64_tr_b16 (4 consecutive k of one column per lane).
+// The loads choose their global chunk per lane to realise the permutation;
+// chunks outside the matrix read as zeros (buffer descriptors).  Two LDS
+// stages; the loads of tile t+1 fly during the
+// MFMAs of tile t; one barrier per tile.  Workgroups are ordered so that the
+// ones an XCD runs (workgroup id mod 8) cover a compact block of C tiles and
+// share A/B panels in that XCD's L2.  The epilogue stages each wave's fp16
+// tile in LDS and writes 16-byte row chunks (accumulating calls add C per
+// element instead, with one rounding of the fp32 sum).
+constexpr int MB_K = 64;  // BK
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from a buffer straight into LDS: lane i writes
+// lds_base + 16 i (lds_base: wave-uniform LDS byte address).  Written as
+// inline assembly so that the compiler does not make every later LDS read
+// wait for these loads (it cannot tell the two stages apart); the kernel
+// waits for them itself (vmcnt) before the barrier that publishes a stage.
+// M0 carries the LDS address; nothing else in the kernels that use this
+// keeps a value in M0.
+DEV void dma16(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(res), "s"(lds_base)
+                 : "memory");
+}
+DEV uint32_t lds_addr(const f16* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const lds_void*)p);
+}
+
+// One operand tile (ROWS x COLS halves as stored in memory; the matrix is
+// nr x nc with leading dimension ld, the tile starts at (r0, c0)) into LDS.
+template <int ROWS, int COLS, bool KCONTIG>
+DEV void tile_to_lds(__amdgpu_buffer_rsrc_t res, int64_t ld, int r0, int c0, int nr, int nc, f16* lds, int wave,
+                     int lane) {
+    constexpr int CPR = COLS / 8;     // chunks per row
+    constexpr int RPI = 64 / CPR;     // rows per wave instruction
+    constexpr int PER = ROWS / RPI / 4;
+    static_assert(PER >= 1 && CPR >= 8, "tile shape");
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+        const int q = wave * PER + t;
+        const int row = q * RPI + lane / CPR, slot = lane % CPR;
+        const int ch = KCONTIG ? (slot ^ (row & 7)) : (slot ^ (2 * (row & 3)));
+        const bool ok = r0 + row < nr && c0 + ch * 8 < nc;
+        const uint32_t off = oob_or(ok, (uint32_t)(((int64_t)(r0 + row) * ld + c0 + ch * 8) * 2));
+        dma16(res, off, lds_addr(lds + q * 512));
+    }
+}
+
+// fragment of a k-contiguous tile: row r, k chunk kc (8 halves)
+DEV half8 frag_k(const f16* t, int r, int kc) {
+    return *reinterpret_cast<const half8*>(t + r * MB_K + ((kc ^ (r & 7)) << 3));
+}
+// fragment of an m/n-contiguous tile (rows of W halves): column block c0
+// (multiple of 16), k rows k0 + 8 g .. +8, through two transposed reads
+template <int W>
+DEV half8 frag_t(const f16* t, int k0, int c0, int g, int trow, int tcol) {
+    auto at = [&](int k) {
+        const int c = c0 + tcol;
+        return t + k * W + ((((c >> 3) ^ (2 * (k & 3))) << 3) | (c & 7));
+    };
+    const int k = k0 + 8 * g + trow;
+    return cat4(lds_read_tr(at(k)), lds_read_tr(at(k + 4)));
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <class F, int... S>
+DEV void static_for_impl(F&& f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, class F>
+DEV void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+DEV int xcd_tile(int w, int total) {
+    if (total % 8) return w;
+    return (w % 8) * (total / 8) + w / 8;  // XCD w%8 gets a contiguous range
+}
+
+template <int BM, int BN, bool TA, bool TB>
+__global__ __launch_bounds__(256, 1) void gemm_mfma(GemmArgs p, int tiles_m, int tiles_n) {
+    constexpr int BK = MB_K, WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int A_EL = BM * BK, B_EL = BN * BK, STAGE = A_EL + B_EL;
+    constexpr int OUT_LD = WN + 8;
+    constexpr int OUT_EL = 4 * WM * OUT_LD;
+    constexpr int LDS_EL = OUT_EL > 2 * STAGE ? OUT_EL : 2 * STAGE;
+    __shared__ __attribute__((aligned(1024))) f16 smem[LDS_EL];
+
+    const int M = p.M, N = p.N, K = p.K;
+    const int bz = blockIdx.z;
+    const f16* A = p.A + (int64_t)bz * p.sA;
+    const f16* B = p.B + (int64_t)bz * p.sB;
+    f16* Cp = p.C + (int64_t)bz * p.sC;
+
+    // tile order: XCD-contiguous ranges, then groups of 4 tile rows
+    const int total = tiles_m * tiles_n;
+    const int t = xcd_tile(blockIdx.x, total);
+    constexpr int GM = 4;
+    const int grp = t / (GM * tiles_n), first = grp * GM, gsz = min(GM, tiles_m - first);
+    const int tm = first + (t % (GM * tiles_n)) % gsz, tn = (t % (GM * tiles_n)) / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
+
+    const __amdgpu_buffer_rsrc_t ares = buf_rsrc(A, (uint32_t)((int64_t)M * K * 2));
+    const __amdgpu_buffer_rsrc_t bres = buf_rsrc(B, (uint32_t)((int64_t)K * N * 2));
+    auto issue = [&](int k0, f16* sa, f16* sb) {
+        if (TA) tile_to_lds<BK, BM, false>(ares, M, k0, m0, K, M, sa, wave, lane);
+        else tile_to_lds<BM, BK, true>(ares, K, m0, k0, M, K, sa, wave, lane);
+        if (TB) tile_to_lds<BN, BK, true>(bres, K, n0, k0, N, K, sb, wave, lane);
+        else tile_to_lds<BK, BN, false>(bres, N, k0, n0, K, N, sb, wave, lane);
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // One LDS tile: 2 k-steps x FM fragment rows, FN MFMAs per row, run as
+    // 2 FM steps.  A fragments are read AD steps ahead (ring of AD + 1); the
+    // B fragments of the second k-step are read during the first, one or
+    // more per step; the scheduling groups pin that order so that the LDS
+    // latency hides behind the MFMAs of earlier steps.
+    constexpr int NA = TA ? 2 : 1, NB = TB ? 1 : 2;  // LDS reads per fragment
+    constexpr int AD = FM >= 4 ? 3 : FM - 1;         // A prefetch distance
+    constexpr int NS = 2 * FM;                       // steps per tile
+    constexpr int BPS = (FN + FM - 1) / FM;          // next-B fragments per step
+    auto ldA = [&](const f16* As, int ks, int i) {
+        return TA ? frag_t<BM>(As, ks * 32, wm0 + 16 * i, g, trow, tcol) : frag_k(As, wm0 + 16 * i + l16, ks * 4 + g);
+    };
+    auto ldB = [&](const f16* Bs, int ks, int j) {
+        return TB ? frag_k(Bs, wn0 + 16 * j + l16, ks * 4 + g) : frag_t<BN>(Bs, ks * 32, wn0 + 16 * j, g, trow, tcol);
+    };
+    auto compute = [&](const f16* As, const f16* Bs) {
+        half8 bf[2][FN], af[AD + 1];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[0][j] = ldB(Bs, 0, j);
+#pragma unroll
+        for (int s2 = 0; s2 < AD; ++s2) af[s2] = ldA(As, s2 / FM, s2 % FM);
+        __builtin_amdgcn_sched_group_barrier(0x100, FN * NB + AD * NA, 0);
+        static_for<NS>([&](auto stc) {
+            constexpr int st = decltype(stc)::value, ks = st / FM, i = st % FM;
+            constexpr bool pre_a = st + AD < NS;
+            constexpr int nb = (ks == 0 && i * BPS < FN) ? (FN - i * BPS >= BPS ? BPS : FN - i * BPS) : 0;
+            if constexpr (pre_a) af[(st + AD) % (AD + 1)] = ldA(As, (st + AD) / FM, (st + AD) % FM);
+#pragma unroll
+            for (int b2 = 0; b2 < nb; ++b2) bf[1][i * BPS + b2] = ldB(Bs, 1, i * BPS + b2);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[st % (AD + 1)], bf[ks][j], acc[i][j]);
+            // this step's LDS reads, then its MFMAs
+            constexpr int nr = (pre_a ? NA : 0) + nb * NB;
+            if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+        });
+    };
+
+    // tile kt lives in stage kt & 1
+    const int KT = (K + BK - 1) / BK;
+    issue(0, smem, smem + A_EL);
+    for (int kt = 0; kt < KT; ++kt) {
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile kt are in LDS
+        __syncthreads();                     // everyone's; the other stage is free again
+        f16* nxt = smem + ((kt + 1) & 1) * STAGE;
+        if (kt + 1 < KT) issue((kt + 1) * BK, nxt, nxt + A_EL);
+        const f16* cur = smem + (kt & 1) * STAGE;
+        compute(cur, cur + A_EL);
+    }
+
+    if (p.acc) {  // C += A B: one rounding of the fp32 sum per element
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = n0 + wn0 + 16 * j + l16;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = m0 + wm0 + 16 * i + 4 * g + e;
+                    if (row < M && col < N) {
+                        f16* dst = Cp + (int64_t)row * N + col;
+                        *dst = (f16)(acc[i][j][e] + (float)*dst);
+                    }
+                }
+            }
+        return;
+    }
+    // stage the wave's tile as fp16 rows, then 16-byte row chunks to C; the
+    // staging area overlaps the stages, which every wave has finished
+    // reading once all have passed this barrier
+    __syncthreads();
+    f16* ot = smem + wave * WM * OUT_LD;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ot[(16 * i + 4 * g + e) * OUT_LD + 16 * j + l16] = (f16)acc[i][j][e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes
+    __builtin_amdgcn_wave_barrier();
+    constexpr int CPR = WN / 8;
+#pragma unroll 4
+    for (int q = lane; q < WM * CPR; q += 64) {
+        const int r = q / CPR, cc = (q % CPR) * 8;
+        const int row = m0 + wm0 + r, col = n0 + wn0 + cc;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ot + r * OUT_LD + cc);
+        if (row < M && col < N) *reinterpret_cast<u32x4*>(Cp + (int64_t)row * N + col) = v;
+    }
+}
+
 // ---- any-alignment fallback: one thread per C element, fp32 FMA ------------
 __global__ __launch_bounds__(256) void gemm_scalar(GemmArgs p, int ta, int tb) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -330,6 +557,22 @@ __global__ __launch_bounds__(256) void gemv_nn(GemmArgs p, int kslice, float* __
     }
 }
 
+template <int BM, int BN, bool TA, bool TB>
+hipError_t launch_mfma(const GemmArgs& a, int batch, hipStream_t st) {
+    const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+    dim3 grid((unsigned)(tm * tn), 1, batch);
+    hipLaunchKernelGGL((gemm_mfma<BM, BN, TA, TB>), grid, dim3(256), 0, st, a, tm, tn);
+    return hipGetLastError();
+}
+
+template <int BM, int BN>
+hipError_t launch_mfma_t(const GemmArgs& a, int batch, bool ta, bool tb, hipStream_t st) {
+    if (!ta && !tb) return launch_mfma<BM, BN, false, false>(a, batch, st);
+    if (!ta && tb) return launch_mfma<BM, BN, false, true>(a, batch, st);
+    if (ta && !tb) return launch_mfma<BM, BN, true, false>(a, batch, st);
+    return launch_mfma<BM, BN, true, true>(a, batch, st);
+}
+
 template <class Cfg, bool TA, bool TB>
 hipError_t launch_tiled(const GemmArgs& a, int batch, hipStream_t st) {
     dim3 grid((a.N + Cfg::BN - 1) / Cfg::BN, (a.M + Cfg::BM - 1) / Cfg::BM, batch);
@@ -423,9 +666,20 @@ int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, h
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) * batch;
     };
-    if (tiles(256, 256) >= cus) e = launch_tiled_t<CfgL>(a, batch, ta, tb, st);
-    else if (tiles(128, 128) >= cus / 2) e = launch_tiled_t<CfgM>(a, batch, ta, tb, st);
-    else e = launch_tiled_t<CfgS>(a, batch, ta, tb, st);
+    // the MFMA kernel addresses each operand through a buffer descriptor
+    const bool fits = (int64_t)a.M * a.K * 2 < INT32_MAX && (int64_t)a.K * a.N * 2 < INT32_MAX &&
+                      (int64_t)a.M * a.N < INT32_MAX;
+    if (fits) {
+        if (tiles(256, 256) >= cus) e = launch_mfma_t<256, 256>(a, batch, ta, tb, st);
+        else if (tiles(128, 128) >= cus / 2) e = launch_mfma_t<128, 128>(a, batch, ta, tb, st);
+        else e = launch_mfma_t<64, 64>(a, batch, ta, tb, st);
+    } else if (tiles(256, 256) >= cus) {
+        e = launch_tiled_t<CfgL>(a, batch, ta, tb, st);
+    } else if (tiles(128, 128) >= cus / 2) {
+        e = launch_tiled_t<CfgM>(a, batch, ta, tb, st);
+    } else {
+        e = launch_tiled_t<CfgS>(a, batch, ta, tb, st);
+    }
     return e == hipSuccess ? EVKHIP_OK : check_hip(e, "gemm launch");
 }
 
