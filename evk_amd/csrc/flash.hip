@@ -421,8 +421,10 @@ __global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
 // ---------------------------------------------------------------------------
 // Forward, key-split (O and the public LSE).
 //
-// Workgroup: 64 query rows and 4 waves.  Wave w owns key chunks w, w+4, ...
-// (32 keys each) of the row tile's key range, for all 64 rows: each wave runs
+// Workgroup: two row tiles of 64 query rows, q and nrg-1-q of one batch (so
+// that under the causal mask every workgroup carries about the same number
+// of key chunks), 4 waves per tile.  Wave w of a tile owns key chunks w, w+4,
+// ... (32 keys each) of the tile's key range, for all 64 rows: each wave runs
 // its own online softmax over its keys and the four partial states
 // (m, l, O) are merged once at the end.  No K/V tile is shared, so nothing
 // is re-read from LDS by several waves and the main loop has no barrier:
@@ -441,10 +443,6 @@ constexpr int KC = 32;  // keys per chunk
 #define FWD_KS_QB 4  // 16-row query blocks per wave (rows per workgroup / 16)
 #endif
 
-// Buffer loads: the base and size live in a scalar resource, offsets past the
-// size read as zero.
-
-
 template <int DH, int QB>
 struct KsLayout {
     static constexpr int ROWS = 16 * QB;         // query rows per workgroup
@@ -459,25 +457,34 @@ struct KsLayout {
 };
 
 template <int DH, int QB, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
+__global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     using L = KsLayout<DH, QB>;
     constexpr int ROWS = L::ROWS;
     constexpr int KS = L::KS, DB = L::DB, VW = L::VW, VPER = L::VPER;
-    __shared__ __attribute__((aligned(16))) float smem_f[L::LDS_BYTES / 4];
-    f16* vslot_all = reinterpret_cast<f16*>(smem_f);
+    __shared__ __attribute__((aligned(16))) float smem_all[2 * (L::LDS_BYTES / 4)];
 
+    // a workgroup runs row tiles nrg-1-q (waves 0-3) and q (waves 4-7) of
+    // one batch: under the causal mask every pair carries about the same
+    // number of key chunks, and both halves share the CU's SIMDs
     const int H = p.H, N = p.N, NH = N * H;
     const int nrg = (NH + ROWS - 1) / ROWS;
-    int rg, b;
-    fwd_block_map(blockIdx.x, nrg, p.B, CAUSAL, round, &rg, &b);
+    const int npair = (nrg + 1) / 2;
+    // consecutive workgroups take consecutive batches: the workgroups an XCD
+    // runs (id mod 8) then share the K/V of few batches in its L2
+    const int b = blockIdx.x % p.B, pq = blockIdx.x / p.B;
+    const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
+    const int rg = half == 0 ? nrg - 1 - pq : pq;
+    const bool active = half == 0 || rg != nrg - 1 - pq;  // odd nrg: the middle tile runs once
+    float* smem_f = smem_all + half * (L::LDS_BYTES / 4);
+    f16* vslot_all = reinterpret_cast<f16*>(smem_f);
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & 3);
     const int l16 = lane & 15, g = lane >> 4;
     const int R0 = rg * ROWS;
     const int last = min(R0 + ROWS - 1, NH - 1);
     const int pmin = R0 / H, pmax = last / H;
     const int kend = CAUSAL ? min(N, pmax + 1) : N;
-    const int nch = (kend + KC - 1) / KC;
+    const int nch = active ? (kend + KC - 1) / KC : 0;
     const float c2 = p.scale_log2;
 
     // K, V of this batch and Q of this row tile through buffer loads: rows
@@ -672,7 +679,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_ks(FlashArgs p, int round) {
         }
         const float l = lt[q];
         const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
-        if (row < NH) {
+        if (active && row < NH) {
             u32x4 o = {pack_h2(a0[0] * inv_l, a0[1] * inv_l), pack_h2(a0[2] * inv_l, a0[3] * inv_l),
                        pack_h2(a1[0] * inv_l, a1[1] * inv_l), pack_h2(a1[2] * inv_l, a1[3] * inv_l)};
             *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
@@ -1558,9 +1565,10 @@ hipError_t launch_fwd(const FlashArgs& a, bool causal, int mode, hipStream_t st)
         // buffer offsets are 32-bit: one batch of K (or V) must stay below 2 GiB
         if (mode == 0 && (int64_t)a.N * DH * 2 < (int64_t)INT32_MAX) {
             constexpr int QB = FWD_KS_QB;
-            dim3 gk((unsigned)(((int64_t)a.N * a.H + 16 * QB - 1) / (16 * QB) * a.B));
-            if (causal) hipLaunchKernelGGL((flash_fwd_ks<DH, QB, true>), gk, dim3(256), 0, st, a, round);
-            else hipLaunchKernelGGL((flash_fwd_ks<DH, QB, false>), gk, dim3(256), 0, st, a, round);
+            const int64_t nrg_ks = ((int64_t)a.N * a.H + 16 * QB - 1) / (16 * QB);
+            dim3 gk((unsigned)((nrg_ks + 1) / 2 * a.B));
+            if (causal) hipLaunchKernelGGL((flash_fwd_ks<DH, QB, true>), gk, dim3(512), 0, st, a);
+            else hipLaunchKernelGGL((flash_fwd_ks<DH, QB, false>), gk, dim3(512), 0, st, a);
             return hipGetLastError();
         }
     }
