@@ -22,6 +22,8 @@
 // Softmax runs in the exp2 domain: s2 = s * scale * log2(e).
 #include "kernels.h"
 
+#include <type_traits>
+
 #include <math.h>
 
 namespace evkhip {
@@ -541,7 +543,12 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     int c = wave;
     if (c < nch) load_chunk(c);
     const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
-    for (; c < nch; c += 4) {
+    // chunks below cu need no mask (all keys in range and, causal, at or
+    // before every row's position); the masked tail runs a separate body so
+    // that the unmasked chunks carry no compare/select per score
+    const int cu = CAUSAL ? min(N / KC, (pmin + 1) / KC) : N / KC;
+    auto chunk = [&](int c, auto mtag) {
+        constexpr bool MASK = decltype(mtag)::value;
         const int key0 = c * KC;
         half8 kf[2][KS];
 #pragma unroll
@@ -567,7 +574,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                 for (int ks = 0; ks < KS; ++ks) s[kb][qb] = mfma16(kf[kb][ks], qf[qb][ks], s[kb][qb]);
             }
         // element j of s[kb][qb]: key key0 + 16 kb + 4 g + j, query row R0 + 16 qb + l16
-        if (key0 + KC > N || (CAUSAL && key0 + KC - 1 > pmin)) {
+        if constexpr (MASK) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 const int lim = (CAUSAL ? min(N - 1, qpos[qb]) : N - 1) - key0 - 4 * g;
@@ -620,7 +627,9 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) oacc[d][qb] = mfma16(vt, pb[qb], oacc[d][qb]);
         }
-    }
+    };
+    for (; c < min(nch, cu); c += 4) chunk(c, std::false_type{});
+    for (; c < nch; c += 4) chunk(c, std::true_type{});
 
     // ---- merge the four waves' partial softmax states ----
     // Merge addresses derive from an opaque copy of the lane id, so the

@@ -13,7 +13,7 @@
 //
 // Skinny kernel (M <= 16, B row-major): bandwidth-bound, streams B once with
 // 16-byte coalesced loads, fp32 accumulation in registers, split-K across
-// workgroups with a deterministic last-arriving-block reduction.
+// workgroups with a deterministic second-pass reduction.
 #include "kernels.h"
 
 #include <algorithm>
@@ -454,108 +454,218 @@ __global__ __launch_bounds__(256) void gemm_scalar(GemmArgs p, int ta, int tb) {
 }
 
 // ---- skinny GEMV: C(M,N) = A(M,K) B(K,N), M <= 16, B row-major -------------
-// Workgroup: 4 waves; columns [n0, n0+512) (lane owns 8 columns); wave w
-// handles rows k0 + w + 4t of the workgroup's K slice.  Partial sums of the
-// 4 waves meet in LDS; the KS slices meet in `part` and the last-arriving
-// workgroup of each column block adds them in slice order.
-constexpr int GV_COLS = 512;
-constexpr int GV_WAVES = 4;
+// Bandwidth-bound on B, which is read exactly once.  Workgroup (cb, ks) owns
+// 64 columns (one 128-byte line of each B row) and the K range
+// [ks*SK_KC, +SK_KC): its 256 threads are 8 column groups of 8 columns x 32
+// row groups, and each thread requests all SK_LD of its 16-byte B loads
+// before it waits, so the whole 64 KB slice is in flight at once.  A's slice
+// is staged in LDS as floats [k][MR]; the A loads go out first and the B
+// loads right after them (the prologue then waits for A only: loads complete
+// in issue order).  The 32 row groups are summed through LDS; with one K
+// range the workgroup writes C, otherwise fp32 partials that gemv_sk_reduce
+// adds in range order (deterministic).
+constexpr int SK_CB = 64;                 // columns per workgroup
+constexpr int SK_RG = 32;                 // row groups
+constexpr int SK_LD = 16;                 // B loads per thread
+constexpr int SK_KC = SK_RG * SK_LD;      // rows per K range (512)
 
 template <int MR>
-__global__ __launch_bounds__(256) void gemv_nn(GemmArgs p, int kslice, float* __restrict__ part,
-                                               unsigned* __restrict__ counters) {
-    __shared__ float red[GV_WAVES][4][GV_COLS];
-    __shared__ float sa[MR][256];
-    __shared__ unsigned s_last;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nblk = blockIdx.x, split = blockIdx.y, bz = blockIdx.z;
-    const int nsplit = gridDim.y;
+__global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) float hv[SK_KC * MR];
+    __shared__ float red[SK_RG * 4 * SK_CB];
     const int M = p.M, N = p.N, K = p.K;
-    const f16* __restrict__ A = p.A + (int64_t)bz * p.sA;
-    const f16* __restrict__ B = p.B + (int64_t)bz * p.sB;
-    f16* __restrict__ Cp = p.C + (int64_t)bz * p.sC;
-    const int n = nblk * GV_COLS + lane * 8;
-    const int kbeg = split * kslice, kend = min(K, kbeg + kslice);
+    const int bz = blockIdx.z, ks = blockIdx.y, nks = gridDim.y;
+    const f16* A = p.A + (int64_t)bz * p.sA;
+    const f16* B = p.B + (int64_t)bz * p.sB;
+    f16* Cp = p.C + (int64_t)bz * p.sC;
+    const int c0 = blockIdx.x * SK_CB, r_lo = ks * SK_KC, r_hi = min(K, r_lo + SK_KC);
+    const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int col = c0 + cg * 8;
+    const bool col_ok = col < N;
+
+    // A slice: MR rows x SK_KC k as 16-byte chunks along k (chunks past K or
+    // M read as zeros)
+    constexpr int ACH = MR * SK_KC / 8, APER = (ACH + 255) / 256;
+    const __amdgpu_buffer_rsrc_t ares = buf_rsrc(A, (uint32_t)((int64_t)M * K * 2));
+    u32x4 av[APER];
+#pragma unroll
+    for (int u = 0; u < APER; ++u) {
+        const int c = threadIdx.x + 256 * u, m = c / (SK_KC / 8), kk = (c % (SK_KC / 8)) * 8;
+        const bool ok = c < ACH && m < M && r_lo + kk < r_hi;
+        av[u] = buf_load16(ares, oob_or(ok, (uint32_t)(((int64_t)m * K + r_lo + kk) * 2)), 0);
+    }
+    asm volatile("" ::: "memory");
+    const __amdgpu_buffer_rsrc_t bres = buf_rsrc(B, (uint32_t)((int64_t)K * N * 2));
+    half8 w[SK_LD];
+#pragma unroll
+    for (int u = 0; u < SK_LD; ++u) {
+        const int i = r_lo + rg + u * SK_RG;
+        w[u] = as_half8(buf_load16(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0));
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < APER; ++u) asm volatile("" : "+v"(av[u]));
+    // A into LDS as hv[k][m] (K-tail chunks were zero-filled by the loads)
+#pragma unroll
+    for (int u = 0; u < APER; ++u) {
+        const int c = threadIdx.x + 256 * u, m = c / (SK_KC / 8), kk = (c % (SK_KC / 8)) * 8;
+        if (c < ACH) {
+            const half8 h = as_half8(av[u]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[(kk + e) * MR + m] = (float)h[e];
+        }
+    }
+    __syncthreads();
 
     float acc[MR][8];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) acc[m][c] = 0.0f;
-
-    for (int kc = kbeg; kc < kend; kc += 256) {
-        __syncthreads();
-        for (int t = threadIdx.x; t < MR * 256; t += 256) {
-            int m = t / 256, kk = kc + (t % 256);
-            sa[m][t % 256] = (m < M && kk < kend) ? (float)A[(int64_t)m * K + kk] : 0.0f;
+        for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < SK_LD; ++u) {
+        const float* hr = hv + (rg + u * SK_RG) * MR;  // zeros past K
+        float hm[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) hm[m] = hr[m];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float wv = (float)w[u][e];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[m][e] += hm[m] * wv;
         }
+    }
+
+    // sum the row groups, 4 rows of A at a time
+#pragma unroll
+    for (int m0 = 0; m0 < MR; m0 += 4) {
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm)
+            if (m0 + mm < MR)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) red[(rg * 4 + mm) * SK_CB + cg * 8 + e] = acc[m0 + mm][e];
         __syncthreads();
-        const int klim = min(256, kend - kc);
-        if (n < N) {
-            int kk = wave;
-#pragma unroll 4
-            for (; kk < klim; kk += GV_WAVES) {
-                u32x4 w = *reinterpret_cast<const u32x4*>(B + (int64_t)(kc + kk) * N + n);
-                half8 h = as_half8(w);
-#pragma unroll
-                for (int m = 0; m < MR; ++m) {
-                    float av = sa[m][kk];
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) acc[m][c] += av * (float)h[c];
+        {
+            const int mm = threadIdx.x / SK_CB, cc = threadIdx.x % SK_CB;
+            const int m = m0 + mm, gc = c0 + cc;
+            float v = 0.0f;
+            for (int r = 0; r < SK_RG; ++r) v += red[(r * 4 + mm) * SK_CB + cc];
+            if (m < M && m < MR && gc < N) {
+                if (nks == 1) {
+                    f16* dst = Cp + (int64_t)m * N + gc;
+                    *dst = (f16)(p.acc ? v + (float)*dst : v);
+                } else {
+                    part[(((int64_t)bz * nks + ks) * M + m) * N + gc] = v;
                 }
             }
         }
+        __syncthreads();
+    }
+}
+
+// Skinny GEMV on the MFMA (4 < M <= 16): the same workgroup slice and
+// loads as gemv_sk, but the arithmetic is v_mfma_f32_16x16x32_f16 with A's
+// 16 (zero-padded) rows as the A operand.  The B slice goes through LDS in
+// two halves of 256 rows (rows of 64 halves, 16-byte chunk c of row r at
+// slot c ^ 2 (r & 3)) and comes back as B operands via ds_read_b64_tr_b16;
+// wave w owns columns c0 + 16 w .. +16 for the whole K range, so no
+// cross-wave sum is needed.
+constexpr int SKM_ALD = SK_KC + 8;  // A row stride in LDS (halves)
+
+__global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) f16 as_[16 * SKM_ALD];
+    __shared__ __attribute__((aligned(16))) f16 bs[(SK_KC / 2) * SK_CB];
+    const int M = p.M, N = p.N, K = p.K;
+    const int bz = blockIdx.z, ks = blockIdx.y, nks = gridDim.y;
+    const f16* A = p.A + (int64_t)bz * p.sA;
+    const f16* B = p.B + (int64_t)bz * p.sB;
+    f16* Cp = p.C + (int64_t)bz * p.sC;
+    const int c0 = blockIdx.x * SK_CB, r_lo = ks * SK_KC, r_hi = min(K, r_lo + SK_KC);
+    const int cg = threadIdx.x & 7, rg = threadIdx.x >> 3;
+    const int col = c0 + cg * 8;
+    const bool col_ok = col < N;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4, trow = l16 >> 2, tcol = (l16 & 3) * 4;
+
+    // A slice: 16 rows (rows >= M read as zeros) x SK_KC k, 16-byte chunks
+    constexpr int ACH = 16 * SK_KC / 8, APER = ACH / 256;
+    const __amdgpu_buffer_rsrc_t ares = buf_rsrc(A, (uint32_t)((int64_t)M * K * 2));
+    u32x4 av[APER];
+#pragma unroll
+    for (int u = 0; u < APER; ++u) {
+        const int c = threadIdx.x + 256 * u, m = c / (SK_KC / 8), kk = (c % (SK_KC / 8)) * 8;
+        const bool ok = m < M && r_lo + kk < r_hi;
+        av[u] = buf_load16(ares, oob_or(ok, (uint32_t)(((int64_t)m * K + r_lo + kk) * 2)), 0);
+    }
+    asm volatile("" ::: "memory");
+    const __amdgpu_buffer_rsrc_t bres = buf_rsrc(B, (uint32_t)((int64_t)K * N * 2));
+    u32x4 w[SK_LD];
+#pragma unroll
+    for (int u = 0; u < SK_LD; ++u) {
+        const int i = r_lo + rg + u * SK_RG;
+        w[u] = buf_load16(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < APER; ++u) {
+        asm volatile("" : "+v"(av[u]));
+        const int c = threadIdx.x + 256 * u, m = c / (SK_KC / 8), kk = (c % (SK_KC / 8)) * 8;
+        *reinterpret_cast<u32x4*>(as_ + m * SKM_ALD + kk) = av[u];
     }
 
-    // reduce the 4 waves, 4 rows of M at a time
-    const bool single = (nsplit == 1);
-    for (int mb = 0; mb < MR; mb += 4) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    constexpr int HALF = SK_LD / 2;  // loads per thread per half (256 rows)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // B rows h*256 .. +256 of the slice into LDS
+#pragma unroll
+        for (int u = 0; u < HALF; ++u) {
+            const int r = rg + u * SK_RG;
+            *reinterpret_cast<u32x4*>(bs + r * SK_CB + ((cg ^ (2 * (r & 3))) << 3)) = w[h * HALF + u];
+        }
         __syncthreads();
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
-            if (mb + mm < MR)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) red[wave][mm][lane * 8 + c] = acc[mb + mm][c];
+        for (int kq = 0; kq < SK_KC / 2 / 32; ++kq) {
+            const half8 af = *reinterpret_cast<const half8*>(as_ + l16 * SKM_ALD + h * (SK_KC / 2) + kq * 32 + 8 * g);
+            auto at = [&](int k) {
+                const int c = wave * 16 + tcol;
+                return bs + k * SK_CB + ((((c >> 3) ^ (2 * (k & 3))) << 3) | (c & 7));
+            };
+            const int k = kq * 32 + 8 * g + trow;
+            const half8 bf = cat4(lds_read_tr(at(k)), lds_read_tr(at(k + 4)));
+            acc = mfma16(af, bf, acc);
+        }
         __syncthreads();
-        for (int t = threadIdx.x; t < 4 * GV_COLS; t += 256) {
-            int mm = t / GV_COLS, col = t % GV_COLS;
-            int m = mb + mm, gc = nblk * GV_COLS + col;
-            if (m >= M || m >= MR || gc >= N) continue;
-            float s = red[0][mm][col] + red[1][mm][col] + red[2][mm][col] + red[3][mm][col];
-            if (single) {
+    }
+    // D: column c0 + 16 wave + l16, rows 4 g + j
+    const int gc = c0 + wave * 16 + l16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = 4 * g + j;
+        if (m < M && gc < N) {
+            if (nks == 1) {
                 f16* dst = Cp + (int64_t)m * N + gc;
-                if (p.acc) s += (float)*dst;
-                *dst = (f16)s;
+                *dst = (f16)(p.acc ? acc[j] + (float)*dst : acc[j]);
             } else {
-                part[(((int64_t)bz * nsplit + split) * M + m) * N + gc] = s;
+                part[(((int64_t)bz * nks + ks) * M + m) * N + gc] = acc[j];
             }
         }
     }
-    if (single) return;
-
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned* cnt = counters + (int64_t)bz * gridDim.x + nblk;
-        unsigned prev = atomicAdd(cnt, 1u);
-        s_last = (prev == (unsigned)(nsplit - 1));
-        if (s_last) *cnt = 0u;  // ready for the next launch
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int t = threadIdx.x; t < M * GV_COLS; t += 256) {
-        int m = t / GV_COLS, gc = nblk * GV_COLS + (t % GV_COLS);
-        if (gc >= N) continue;
-        float s = 0.0f;
-        for (int sp = 0; sp < nsplit; ++sp)
-            s += __hip_atomic_load(part + (((int64_t)bz * nsplit + sp) * M + m) * N + gc,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        f16* dst = Cp + (int64_t)m * N + gc;
-        if (p.acc) s += (float)*dst;
-        *dst = (f16)s;
-    }
 }
+
+// C = sum over the K ranges of the partials, in range order (+ C when
+// accumulating); one thread per element.
+__global__ __launch_bounds__(256) void gemv_sk_reduce(GemmArgs p, const float* __restrict__ part, int nks) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int bz = blockIdx.y;
+    const int64_t MN = (int64_t)p.M * p.N;
+    if (idx >= MN) return;
+    float v = 0.0f;
+    for (int s2 = 0; s2 < nks; ++s2) v += part[((int64_t)bz * nks + s2) * MN + idx];
+    f16* dst = p.C + (int64_t)bz * p.sC + idx;
+    *dst = (f16)(p.acc ? v + (float)*dst : v);
+}
+
 
 template <int BM, int BN, bool TA, bool TB>
 hipError_t launch_mfma(const GemmArgs& a, int batch, hipStream_t st) {
@@ -592,12 +702,10 @@ using CfgL = TileCfg<256, 256, 64, 2, 2>;  // 4 waves of 128x128
 using CfgM = TileCfg<128, 128, 64, 2, 2>;  // 4 waves of 64x64
 using CfgS = TileCfg<64, 64, 64, 2, 2>;    // 4 waves of 32x32
 
-// Library workspace for the split-K GEMV (grow-only).
+// Library workspace for the split-K GEMV partials (grow-only).
 struct GemvWorkspace {
     float* part = nullptr;
     size_t part_elems = 0;
-    unsigned* counters = nullptr;
-    size_t n_counters = 0;
 };
 GemvWorkspace g_gemv_ws;
 
@@ -605,23 +713,16 @@ GemvWorkspace g_gemv_ws;
 
 void gemm_free_workspace() {
     if (g_gemv_ws.part) (void)hipFree(g_gemv_ws.part);
-    if (g_gemv_ws.counters) (void)hipFree(g_gemv_ws.counters);
     g_gemv_ws = GemvWorkspace{};
 }
 
-static int gemv_workspace(size_t part_elems, size_t n_counters) {
+static int gemv_workspace(size_t part_elems) {
     if (part_elems > g_gemv_ws.part_elems) {
         if (g_gemv_ws.part) EVK_HIP(hipFree(g_gemv_ws.part));
         g_gemv_ws.part = nullptr;
+        g_gemv_ws.part_elems = 0;
         EVK_HIP(hipMalloc(&g_gemv_ws.part, part_elems * sizeof(float)));
         g_gemv_ws.part_elems = part_elems;
-    }
-    if (n_counters > g_gemv_ws.n_counters) {
-        if (g_gemv_ws.counters) EVK_HIP(hipFree(g_gemv_ws.counters));
-        g_gemv_ws.counters = nullptr;
-        EVK_HIP(hipMalloc(&g_gemv_ws.counters, n_counters * sizeof(unsigned)));
-        EVK_HIP(hipMemset(g_gemv_ws.counters, 0, n_counters * sizeof(unsigned)));
-        g_gemv_ws.n_counters = n_counters;
     }
     return EVKHIP_OK;
 }
@@ -638,29 +739,30 @@ int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, h
         e = hipGetLastError();
         return e == hipSuccess ? EVKHIP_OK : check_hip(e, "gemm_scalar launch");
     }
-    if (a.M <= 16 && !ta && !tb && a.K > 0) {
-        const int nblk = (a.N + GV_COLS - 1) / GV_COLS;
-        const int cus = device_cu_count();
-        // aim for ~2 workgroups per CU; K slices are multiples of 256 rows
-        int want = std::max(1, (2 * cus + nblk * batch - 1) / (nblk * batch));
-        int kslice = std::max(256, ((a.K + want - 1) / want + 255) / 256 * 256);
-        int nsplit = (a.K + kslice - 1) / kslice;
+    if (a.M <= 16 && !ta && !tb && a.K > 0 && (int64_t)a.K * a.N * 2 < INT32_MAX &&
+        (int64_t)a.M * a.K * 2 < INT32_MAX) {
+        const int ncb = (a.N + SK_CB - 1) / SK_CB;
+        const int nks = (a.K + SK_KC - 1) / SK_KC;
         float* part = nullptr;
-        unsigned* cnt = nullptr;
-        if (nsplit > 1) {
-            int rc = gemv_workspace((size_t)batch * nsplit * a.M * a.N, (size_t)batch * nblk);
+        if (nks > 1) {
+            int rc = gemv_workspace((size_t)batch * nks * a.M * a.N);
             if (rc) return rc;
             part = g_gemv_ws.part;
-            cnt = g_gemv_ws.counters;
         }
-        dim3 grid(nblk, nsplit, batch);
-        if (a.M <= 1) hipLaunchKernelGGL(gemv_nn<1>, grid, dim3(256), 0, st, a, kslice, part, cnt);
-        else if (a.M <= 2) hipLaunchKernelGGL(gemv_nn<2>, grid, dim3(256), 0, st, a, kslice, part, cnt);
-        else if (a.M <= 4) hipLaunchKernelGGL(gemv_nn<4>, grid, dim3(256), 0, st, a, kslice, part, cnt);
-        else if (a.M <= 8) hipLaunchKernelGGL(gemv_nn<8>, grid, dim3(256), 0, st, a, kslice, part, cnt);
-        else hipLaunchKernelGGL(gemv_nn<16>, grid, dim3(256), 0, st, a, kslice, part, cnt);
+        dim3 grid(ncb, nks, batch);
+        if (a.M <= 1) hipLaunchKernelGGL(gemv_sk<1>, grid, dim3(256), 0, st, a, part);
+        else if (a.M <= 2) hipLaunchKernelGGL(gemv_sk<2>, grid, dim3(256), 0, st, a, part);
+        else if (a.M <= 4) hipLaunchKernelGGL(gemv_sk<4>, grid, dim3(256), 0, st, a, part);
+        else hipLaunchKernelGGL(gemv_mf, grid, dim3(256), 0, st, a, part);
         e = hipGetLastError();
-        return e == hipSuccess ? EVKHIP_OK : check_hip(e, "gemv launch");
+        if (e != hipSuccess) return check_hip(e, "gemv launch");
+        if (nks > 1) {
+            dim3 rgrid((unsigned)(((int64_t)a.M * a.N + 255) / 256), batch);
+            hipLaunchKernelGGL(gemv_sk_reduce, rgrid, dim3(256), 0, st, a, (const float*)part, nks);
+            e = hipGetLastError();
+            if (e != hipSuccess) return check_hip(e, "gemv reduce launch");
+        }
+        return EVKHIP_OK;
     }
     const int64_t cus = device_cu_count();
     auto tiles = [&](int bm, int bn) {

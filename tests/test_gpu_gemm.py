@@ -104,19 +104,36 @@ def test_skinny_gemv_config5(dev, orc, M):
     b = orc.uniform_f16((K, N), 510)
     got = run_mm(evk, dev, a, b, (M, N))
     assert_close_f16(got, orc.matmul(a, b), what=f"gemv M={M}")
-    # second call reuses the split-K counters: must give identical bits
+    # second call reuses the split-K workspace: must give identical bits
     got2 = run_mm(evk, dev, a, b, (M, N))
     assert np.array_equal(got, got2)
 
 
 def test_skinny_acc_and_small(dev, orc):
     import evk_amd as evk
-    for (M, K, N) in [(1, 768, 2304), (3, 3072, 768), (2, 8, 16), (1, 4096, 32000)]:
+    # M <= 4 runs on the VALU kernel, 4 < M <= 16 on the MFMA one; K ranges of
+    # 512 rows: single-range (direct C write) and ragged split-K cases
+    for (M, K, N) in [(1, 768, 2304), (3, 3072, 768), (2, 8, 16), (1, 4096, 32000),
+                      (5, 512, 64), (8, 1000, 136), (16, 520, 2000), (12, 4096, 1032), (9, 24, 40)]:
         a = orc.uniform_f16((M, K), 71 + K)
         b = orc.uniform_f16((K, N), 72 + N)
         c0 = orc.uniform_f16((M, N), 73)
         got = run_mm(evk, dev, a, b, None, acc=True, c0=c0)
         assert_close_f16(got, orc.matmul(a, b, c=c0, acc_c=True), what=f"gemv acc {M}x{K}x{N}")
+
+
+def test_skinny_batched(dev, orc):
+    """Batched skinny products: per-batch A over a shared B (MFMA kernel,
+    split-K), and a shared A over per-batch B (VALU kernel)."""
+    import evk_amd as evk
+    a = orc.uniform_f16((3, 12, 1040), 81)
+    b = orc.uniform_f16((1040, 200), 82)
+    got = run_mm(evk, dev, a, b, (3, 12, 200))
+    assert_close_f16(got, orc.matmul(a, b, out_shape=(3, 12, 200)), what="batched A")
+    a1 = orc.uniform_f16((1, 520), 83)
+    b3 = orc.uniform_f16((2, 520, 72), 84)
+    got = run_mm(evk, dev, a1, b3, (2, 1, 72))
+    assert_close_f16(got, orc.matmul(a1, b3, out_shape=(2, 1, 72)), what="batched B")
 
 
 def _rows_check(orc, a, b, got, rows):
