@@ -498,14 +498,29 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     f16* vslot = vslot_all + wave * L::VSLOT;
 
     // Q^T B operands: query R0 + 16 qb + l16, dh [32 ks + 8 g, +8)
+    // the tile's Q goes through LDS once (each wave of the half loads a
+    // quarter), then every wave reads its fragments from there
     half8 qf[QB][KS];
     int qpos[QB];
+    {
+        constexpr int QPIECES = ROWS * DH / 8;           // 16-byte pieces of the tile
+        constexpr int QPER = QPIECES / 256;
+        f16* qs = vslot_all;                              // [ROWS][DH + 8]
+        const int ht = threadIdx.x & 255;
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-        qpos[qb] = min(R0 + qb * 16 + l16, NH - 1) / H;
+        for (int u = 0; u < QPER; ++u) {
+            const int pc = ht + 256 * u, r = pc / (DH / 8), cc = (pc % (DH / 8)) * 8;
+            *reinterpret_cast<u32x4*>(qs + r * (DH + 8) + cc) = buf_load16(qres, (uint32_t)(r * DH + cc) * 2, 0);
+        }
+        __syncthreads();
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qf[qb][ks] = as_half8(buf_load16(qres, (uint32_t)((qb * 16 + l16) * DH + ks * 32 + g * 8) * 2, 0));
+        for (int qb = 0; qb < QB; ++qb) {
+            qpos[qb] = min(R0 + qb * 16 + l16, NH - 1) / H;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                qf[qb][ks] = *reinterpret_cast<const half8*>(qs + (qb * 16 + l16) * (DH + 8) + ks * 32 + g * 8);
+        }
+        __syncthreads();  // the V slots reuse this space
     }
 
     floatx4 oacc[DB][QB];
