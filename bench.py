@@ -4,7 +4,8 @@
 
 Headline: causal MQA flash-attention forward,
 fp16, B=4, H=8, S=1024, Dh=64, inputs resident in HBM.  A step is one
-evk::ai::flash_attention call over the whole batch (one kernel launch);
+evk::ai::flash_attention call over the whole batch (one kernel launch); the
+timed steps run as one captured HIP graph, so host launch cost is excluded;
 TFLOP/s uses the causal convention 2*B*H*S^2*Dh = 4.295 GFLOP per step.
 `roofline` compares the kernel's achieved TFLOP/s with MI355X's dense fp16
 MFMA peak; `traffic` is the HBM bytes per launch measured with rocprofv3
@@ -61,20 +62,55 @@ def profile_copy():
     print(f"copied {n} bytes x 20")
 
 
-def timed(fn, steps, warmup):
-    """Average ms per call of fn() over `steps` back-to-back calls on torch's
-    current stream (the stream the kernels are launched on), HIP events."""
+def timed(fn, steps, warmup, check=None):
+    """Average ms per call of fn() over exactly `steps` back-to-back calls.
+
+    After `warmup` eager calls, the `steps` calls are captured into one HIP
+    graph (torch.cuda.CUDAGraph: the library launches on torch's current
+    stream, which is the capture stream during capture) and the graph is
+    replayed once between two HIP events on the current stream, so that the
+    timed region holds the kernels without host launch gaps.  `check`
+    returns the output tensors; those of the replay must equal those of the
+    last eager call bit for bit (the kernels are deterministic), else the
+    eager launches are timed instead.  Capture failures also fall back to
+    eager launches."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(steps):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps
+    want = [t.clone() for t in check()] if check else None
+    graph = None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                fn()
+        torch.cuda.synchronize()
+    except Exception as ex:  # capture unsupported here: time eager launches
+        print(f"bench.py: graph capture failed ({ex}); timing eager launches", file=sys.stderr)
+        graph = None
+
+    def run():
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        if graph is not None:
+            graph.replay()
+        else:
+            for _ in range(steps):
+                fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps
+
+    ms = run()
+    if graph is not None and check is not None:
+        if not all(torch.equal(a, b) for a, b in zip(check(), want)):
+            print("bench.py: graph replay differs from the eager result; timing eager launches",
+                  file=sys.stderr)
+            graph = None
+            ms = run()
+    return ms
 
 
 def read_traffic(name):
@@ -123,7 +159,8 @@ def main():
     L = torch.empty((B, H, S), dtype=torch.float32, device=dev)
     flops = 2.0 * B * H * S * S * Dh
     torch.cuda.synchronize()
-    ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup)
+    ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup,
+               check=lambda: (O, L))
     tflops = flops / (ms * 1e-3) / 1e12
     traffic = read_traffic("flash_fwd_c2_traffic.txt")
 
@@ -159,7 +196,7 @@ def main():
         a = to_dev(orc.uniform_f16((gm, gk), seed))
         b = to_dev(orc.uniform_f16((gk, gn), seed + 1))
         c = torch.empty((gm, gn), dtype=torch.float16, device=dev)
-        ms_ = timed(lambda: evk.matmul(a, b, c), steps, 5)
+        ms_ = timed(lambda: evk.matmul(a, b, c), steps, 5, check=lambda: (c,))
         del a, b, c
         return ms_
 
@@ -182,7 +219,7 @@ def main():
         dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
         evk.flash_attention(Q, K, V, O, causal=True, lse=L)
         ms_ = timed(lambda: evk.flash_attention_bwd(Q, K, V, O, G, dQ, dK, dV, causal=True, lse=L),
-                    100, 10)
+                    100, 10, check=lambda: (dQ, dK, dV))
         tf = 2.5 * flops / (ms_ * 1e-3) / 1e12
         sec["flash_bwd_c3"] = {"ms": round(ms_, 4), "TFLOP/s": round(tf, 1),
                                "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4),
@@ -203,7 +240,7 @@ def main():
             tok[0] = first  # same 32 steps every repetition (positions 1024..1055)
             evk.model_decode(cfg, w, cache, tok, 32, 1024, logits)
 
-        ms32 = timed(run32, 5, 1)
+        ms32 = timed(run32, 5, 1, check=lambda: (tok, logits))
         d, hid, V_ = 768, 3072, 32000
         layer_bytes = 12 * (d * 3 * d + d * d + 2 * d * hid) * 2
         kv_bytes = sum(12 * 2 * (1024 + s + 1) * d * 2 for s in range(32)) / 32

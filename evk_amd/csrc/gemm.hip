@@ -221,8 +221,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled(GemmArgs p) {
 //     ds_read_b64_tr_b16 (4 consecutive k of one column per lane).
 // The loads choose their global chunk per lane to realise the permutation;
 // chunks outside the matrix read as zeros (buffer descriptors).  Two LDS
-// stages; the loads of tile t+1 fly during the
-// MFMAs of tile t; one barrier per tile.  Workgroups are ordered so that the
+// stages for 256x256 tiles, four for smaller ones: the loads of the next
+// tiles fly during the MFMAs of tile t; one barrier per tile.  Workgroups are ordered so that the
 // ones an XCD runs (workgroup id mod 8) cover a compact block of C tiles and
 // share A/B panels in that XCD's L2.  The epilogue stages each wave's fp16
 // tile in LDS and writes 16-byte row chunks (accumulating calls add C per
@@ -299,13 +299,32 @@ DEV int xcd_tile(int w, int total) {
     return (w % 8) * (total / 8) + w / 8;  // XCD w%8 gets a contiguous range
 }
 
+// LDS stages of gemm_mfma: two for 256x256 tiles (128 KB), four for the
+// smaller tiles, whose short K loops need more tiles in flight.
+template <int BM>
+constexpr int mfma_stages() { return BM >= 256 ? 2 : 4; }
+
+// s_waitcnt with vmcnt(n) (n < 64) and the other counters left alone
+DEV void wait_vmcnt(int n) {
+    switch (n) {
+#define EVK_VMCNT_CASE(v) \
+    case v: __builtin_amdgcn_s_waitcnt(((v) & 15) | (((v) >> 4) << 14) | 0x0f70); break;
+        EVK_VMCNT_CASE(0) EVK_VMCNT_CASE(4) EVK_VMCNT_CASE(8) EVK_VMCNT_CASE(12) EVK_VMCNT_CASE(16)
+        EVK_VMCNT_CASE(24) EVK_VMCNT_CASE(32)
+#undef EVK_VMCNT_CASE
+        default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+    }
+}
+
 template <int BM, int BN, bool TA, bool TB>
 __global__ __launch_bounds__(256, 1) void gemm_mfma(GemmArgs p, int tiles_m, int tiles_n) {
     constexpr int BK = MB_K, WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
     constexpr int A_EL = BM * BK, B_EL = BN * BK, STAGE = A_EL + B_EL;
+    constexpr int NST = mfma_stages<BM>();
+    constexpr int LPT = (BM * BK / 512 + BN * BK / 512) / 4;  // DMA loads per wave per tile
     constexpr int OUT_LD = WN + 8;
     constexpr int OUT_EL = 4 * WM * OUT_LD;
-    constexpr int LDS_EL = OUT_EL > 2 * STAGE ? OUT_EL : 2 * STAGE;
+    constexpr int LDS_EL = OUT_EL > NST * STAGE ? OUT_EL : NST * STAGE;
     __shared__ __attribute__((aligned(1024))) f16 smem[LDS_EL];
 
     const int M = p.M, N = p.N, K = p.K;
@@ -381,15 +400,21 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(GemmArgs p, int tiles_m, int
         });
     };
 
-    // tile kt lives in stage kt & 1
+    // tile kt lives in stage kt % NST; NST-1 tiles are in flight
     const int KT = (K + BK - 1) / BK;
-    issue(0, smem, smem + A_EL);
+#pragma unroll
+    for (int t2 = 0; t2 < NST - 1; ++t2)
+        if (t2 < KT) issue(t2 * BK, smem + t2 * STAGE, smem + t2 * STAGE + A_EL);
     for (int kt = 0; kt < KT; ++kt) {
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of tile kt are in LDS
-        __syncthreads();                     // everyone's; the other stage is free again
-        f16* nxt = smem + ((kt + 1) & 1) * STAGE;
-        if (kt + 1 < KT) issue((kt + 1) * BK, nxt, nxt + A_EL);
-        const f16* cur = smem + (kt & 1) * STAGE;
+        // this wave's loads of tile kt are in LDS once at most the loads of
+        // the younger tiles in flight remain (loads complete in order)
+        wait_vmcnt(LPT * min(NST - 2, KT - 1 - kt));
+        __syncthreads();  // everyone's; the stage of tile kt-1 is free again
+        if (kt + NST - 1 < KT) {
+            f16* nxt = smem + ((kt + NST - 1) % NST) * STAGE;
+            issue((kt + NST - 1) * BK, nxt, nxt + A_EL);
+        }
+        const f16* cur = smem + (kt % NST) * STAGE;
         compute(cur, cur + A_EL);
     }
 
