@@ -608,7 +608,9 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                            fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
             grow |= mx[qb] > m_ref[qb] + RESCALE_LOG2;
         }
-        if (__any(grow)) {
+        // rare (lazy rescale): a real branch, kept out of the common path
+        if (__builtin_expect(__any(grow), 0)) {
+            asm volatile("" ::: "memory");
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 float m = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
