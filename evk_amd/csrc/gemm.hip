@@ -13,7 +13,7 @@
 //
 // Skinny kernel (M <= 16, B row-major): bandwidth-bound, streams B once with
 // 16-byte coalesced loads, fp32 accumulation in registers, split-K across
-// workgroups with a deterministic second-pass reduction.
+// workgroups with a deterministic last-arriving-workgroup reduction.
 #include "kernels.h"
 
 #include <algorithm>
@@ -487,15 +487,40 @@ __global__ __launch_bounds__(256) void gemm_scalar(GemmArgs p, int ta, int tb) {
 // is staged in LDS as floats [k][MR]; the A loads go out first and the B
 // loads right after them (the prologue then waits for A only: loads complete
 // in issue order).  The 32 row groups are summed through LDS; with one K
-// range the workgroup writes C, otherwise fp32 partials that gemv_sk_reduce
-// adds in range order (deterministic).
+// range the workgroup writes C, otherwise fp32 partials that the column
+// block's last-arriving workgroup adds in range order (deterministic).
 constexpr int SK_CB = 64;                 // columns per workgroup
 constexpr int SK_RG = 32;                 // row groups
 constexpr int SK_LD = 16;                 // B loads per thread
 constexpr int SK_KC = SK_RG * SK_LD;      // rows per K range (512)
 
+// The K ranges of a column block meet in the workgroup that arrives last
+// (agent-scope partial stores and counter, no fences); it adds the partials
+// in range order, so the result does not depend on arrival order.
+DEV void gemv_finish(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
+    const int M = p.M, N = p.N, bz = blockIdx.z, nks = gridDim.y;
+    if (!arrive_last(cnt + bz * gridDim.x + blockIdx.x, nks)) return;
+    f16* Cp = p.C + (int64_t)bz * p.sC;
+    for (int idx = threadIdx.x; idx < M * SK_CB; idx += 256) {
+        const int m = idx / SK_CB, gc = c0 + idx % SK_CB;
+        if (gc >= N) continue;
+        const float* src = part + ((int64_t)bz * nks * M + m) * N + gc;
+        const int64_t stride = (int64_t)M * N;
+        float v = 0.0f;
+        for (int s0 = 0; s0 < nks; s0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = (s0 + u < nks) ? ld_ag(src + (s0 + u) * stride) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        f16* dst = Cp + (int64_t)m * N + gc;
+        *dst = (f16)(p.acc ? v + (float)*dst : v);
+    }
+}
+
 template <int MR>
-__global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ part) {
+__global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ part, unsigned* cnt) {
     __shared__ __attribute__((aligned(16))) float hv[SK_KC * MR];
     __shared__ float red[SK_RG * 4 * SK_CB];
     const int M = p.M, N = p.N, K = p.K;
@@ -580,12 +605,13 @@ __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ p
                     f16* dst = Cp + (int64_t)m * N + gc;
                     *dst = (f16)(p.acc ? v + (float)*dst : v);
                 } else {
-                    part[(((int64_t)bz * nks + ks) * M + m) * N + gc] = v;
+                    st_ag(part + (((int64_t)bz * nks + ks) * M + m) * N + gc, v);
                 }
             }
         }
         __syncthreads();
     }
+    if (nks > 1) gemv_finish(p, part, cnt, c0);
 }
 
 // Skinny GEMV on the MFMA (4 < M <= 16): the same workgroup slice and
@@ -597,7 +623,7 @@ __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ p
 // cross-wave sum is needed.
 constexpr int SKM_ALD = SK_KC + 8;  // A row stride in LDS (halves)
 
-__global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ part) {
+__global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ part, unsigned* cnt) {
     __shared__ __attribute__((aligned(16))) f16 as_[16 * SKM_ALD];
     __shared__ __attribute__((aligned(16))) f16 bs[(SK_KC / 2) * SK_CB];
     const int M = p.M, N = p.N, K = p.K;
@@ -672,24 +698,13 @@ __global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ p
                 f16* dst = Cp + (int64_t)m * N + gc;
                 *dst = (f16)(p.acc ? acc[j] + (float)*dst : acc[j]);
             } else {
-                part[(((int64_t)bz * nks + ks) * M + m) * N + gc] = acc[j];
+                st_ag(part + (((int64_t)bz * nks + ks) * M + m) * N + gc, acc[j]);
             }
         }
     }
+    if (nks > 1) gemv_finish(p, part, cnt, c0);
 }
 
-// C = sum over the K ranges of the partials, in range order (+ C when
-// accumulating); one thread per element.
-__global__ __launch_bounds__(256) void gemv_sk_reduce(GemmArgs p, const float* __restrict__ part, int nks) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int bz = blockIdx.y;
-    const int64_t MN = (int64_t)p.M * p.N;
-    if (idx >= MN) return;
-    float v = 0.0f;
-    for (int s2 = 0; s2 < nks; ++s2) v += part[((int64_t)bz * nks + s2) * MN + idx];
-    f16* dst = p.C + (int64_t)bz * p.sC + idx;
-    *dst = (f16)(p.acc ? v + (float)*dst : v);
-}
 
 
 template <int BM, int BN, bool TA, bool TB>
@@ -727,10 +742,14 @@ using CfgL = TileCfg<256, 256, 64, 2, 2>;  // 4 waves of 128x128
 using CfgM = TileCfg<128, 128, 64, 2, 2>;  // 4 waves of 64x64
 using CfgS = TileCfg<64, 64, 64, 2, 2>;    // 4 waves of 32x32
 
-// Library workspace for the split-K GEMV partials (grow-only).
+// Library workspace for the split-K GEMV (grow-only): partials, and the
+// per-column-block arrival counters in an allocation of their own (zeroed
+// once; the last arrival of every launch leaves its counter at zero).
 struct GemvWorkspace {
     float* part = nullptr;
     size_t part_elems = 0;
+    unsigned* counters = nullptr;
+    size_t n_counters = 0;
 };
 GemvWorkspace g_gemv_ws;
 
@@ -738,16 +757,25 @@ GemvWorkspace g_gemv_ws;
 
 void gemm_free_workspace() {
     if (g_gemv_ws.part) (void)hipFree(g_gemv_ws.part);
+    if (g_gemv_ws.counters) (void)hipFree(g_gemv_ws.counters);
     g_gemv_ws = GemvWorkspace{};
 }
 
-static int gemv_workspace(size_t part_elems) {
+static int gemv_workspace(size_t part_elems, size_t n_counters, hipStream_t st) {
     if (part_elems > g_gemv_ws.part_elems) {
         if (g_gemv_ws.part) EVK_HIP(hipFree(g_gemv_ws.part));
         g_gemv_ws.part = nullptr;
         g_gemv_ws.part_elems = 0;
         EVK_HIP(hipMalloc(&g_gemv_ws.part, part_elems * sizeof(float)));
         g_gemv_ws.part_elems = part_elems;
+    }
+    if (n_counters > g_gemv_ws.n_counters) {
+        if (g_gemv_ws.counters) EVK_HIP(hipFree(g_gemv_ws.counters));
+        g_gemv_ws.counters = nullptr;
+        g_gemv_ws.n_counters = 0;
+        EVK_HIP(hipMalloc(&g_gemv_ws.counters, n_counters * sizeof(unsigned)));
+        EVK_HIP(hipMemsetAsync(g_gemv_ws.counters, 0, n_counters * sizeof(unsigned), st));
+        g_gemv_ws.n_counters = n_counters;
     }
     return EVKHIP_OK;
 }
@@ -769,25 +797,20 @@ int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, h
         const int ncb = (a.N + SK_CB - 1) / SK_CB;
         const int nks = (a.K + SK_KC - 1) / SK_KC;
         float* part = nullptr;
+        unsigned* cnt = nullptr;
         if (nks > 1) {
-            int rc = gemv_workspace((size_t)batch * nks * a.M * a.N);
+            int rc = gemv_workspace((size_t)batch * nks * a.M * a.N, (size_t)batch * ncb, st);
             if (rc) return rc;
             part = g_gemv_ws.part;
+            cnt = g_gemv_ws.counters;
         }
         dim3 grid(ncb, nks, batch);
-        if (a.M <= 1) hipLaunchKernelGGL(gemv_sk<1>, grid, dim3(256), 0, st, a, part);
-        else if (a.M <= 2) hipLaunchKernelGGL(gemv_sk<2>, grid, dim3(256), 0, st, a, part);
-        else if (a.M <= 4) hipLaunchKernelGGL(gemv_sk<4>, grid, dim3(256), 0, st, a, part);
-        else hipLaunchKernelGGL(gemv_mf, grid, dim3(256), 0, st, a, part);
+        if (a.M <= 1) hipLaunchKernelGGL(gemv_sk<1>, grid, dim3(256), 0, st, a, part, cnt);
+        else if (a.M <= 2) hipLaunchKernelGGL(gemv_sk<2>, grid, dim3(256), 0, st, a, part, cnt);
+        else if (a.M <= 4) hipLaunchKernelGGL(gemv_sk<4>, grid, dim3(256), 0, st, a, part, cnt);
+        else hipLaunchKernelGGL(gemv_mf, grid, dim3(256), 0, st, a, part, cnt);
         e = hipGetLastError();
-        if (e != hipSuccess) return check_hip(e, "gemv launch");
-        if (nks > 1) {
-            dim3 rgrid((unsigned)(((int64_t)a.M * a.N + 255) / 256), batch);
-            hipLaunchKernelGGL(gemv_sk_reduce, rgrid, dim3(256), 0, st, a, (const float*)part, nks);
-            e = hipGetLastError();
-            if (e != hipSuccess) return check_hip(e, "gemv reduce launch");
-        }
-        return EVKHIP_OK;
+        return e == hipSuccess ? EVKHIP_OK : check_hip(e, "gemv launch");
     }
     const int64_t cus = device_cu_count();
     auto tiles = [&](int bm, int bn) {

@@ -90,24 +90,6 @@ struct DecArgs {
     unsigned* cnt;     // counters (zero between launches)
 };
 
-DEV void st_ag(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV float ld_ag(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV void st_ag(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV uint32_t ld_ag(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-
-DEV bool arrive_last(unsigned* cnt, unsigned total) {
-    __shared__ unsigned s_last;
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev + 1 == total);
-        if (s_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
-    }
-    __syncthreads();
-    return s_last;
-}
-
 enum { PRO_PLAIN = 0, PRO_RMS = 1, PRO_EMBED_RMS = 2, PRO_ATTN = 3, PRO_GELU = 4 };
 enum { EPI_PART = 0, EPI_HEAD = 1 };
 constexpr int ATT_SMAX = 16;  // attention splits per head, at most
