@@ -1182,25 +1182,30 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
 }
 
 // lse2_rows / d_rows from a saved LSE and O: D_i = rowsum(dO_i * O_i).
+// DH/8 lanes per row, one 16-byte piece of O and of dO each (coalesced),
+// summed across the row's lanes with shuffles.
 template <int DH>
 __global__ __launch_bounds__(256) void flash_bwd_pre(FlashArgs p) {
+    constexpr int LPR = DH / 8;  // lanes per row
     const int NH = p.N * p.H;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)p.B * NH) return;
-    const int b = (int)(idx / NH), r = (int)(idx % NH);
-    const f16* o = p.o + idx * DH;
-    const f16* g = p.dO + idx * DH;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t idx = t / LPR;  // flattened (batch, row)
+    const int part = (int)(t % LPR);
+    const bool ok = idx < (int64_t)p.B * NH;
     float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < DH / 8; ++c) {
-        half8 x = *reinterpret_cast<const half8*>(o + c * 8);
-        half8 y = *reinterpret_cast<const half8*>(g + c * 8);
+    if (ok) {
+        const half8 x = *reinterpret_cast<const half8*>(p.o + idx * DH + part * 8);
+        const half8 y = *reinterpret_cast<const half8*>(p.dO + idx * DH + part * 8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
     }
-    p.d_rows[idx] = acc;
-    const float l = p.lse[((int64_t)b * p.H + (r % p.H)) * p.N + r / p.H];
-    p.lse2_rows[idx] = l * kLog2e;
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (ok && part == 0) {
+        const int b = (int)(idx / NH), r = (int)(idx % NH);
+        p.d_rows[idx] = acc;
+        p.lse2_rows[idx] = p.lse[((int64_t)b * p.H + (r % p.H)) * p.N + r / p.H] * kLog2e;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1612,7 +1617,7 @@ template <int DH>
 hipError_t launch_bwd(const FlashArgs& a, bool causal, bool have_lse, hipStream_t st) {
     const int NH = a.N * a.H;
     if (have_lse) {
-        dim3 g((unsigned)(((int64_t)a.B * NH + 255) / 256));
+        dim3 g((unsigned)(((int64_t)a.B * NH * (DH / 8) + 255) / 256));
         hipLaunchKernelGGL(flash_bwd_pre<DH>, g, dim3(256), 0, st, a);
     } else {
         hipError_t e = launch_fwd<DH>(a, causal, 1, st);
@@ -1635,7 +1640,7 @@ template <int DH>
 hipError_t launch_bwd_split(const FlashArgs& a, bool causal, float* parts, int parts_per_batch,
                             hipStream_t st) {
     const int NH = a.N * a.H;
-    dim3 gp((unsigned)(((int64_t)a.B * NH + 255) / 256));
+    dim3 gp((unsigned)(((int64_t)a.B * NH * (DH / 8) + 255) / 256));
     hipLaunchKernelGGL(flash_bwd_pre<DH>, gp, dim3(256), 0, st, a);
     dim3 gkv((unsigned)(a.B * parts_per_batch));
     dim3 gq((unsigned)((NH + 63) / 64 * a.B));
