@@ -741,7 +741,7 @@ typedef int intx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BKB = 128;       // keys per workgroup (4 waves x 32)
 constexpr int BRC = 32;        // flattened query rows per chunk
-constexpr int PART_CHUNKS = 12;
+constexpr int PART_CHUNKS = 16;
 
 // Chunks of flattened rows that key block kb of a batch interacts with.
 __host__ __device__ inline int bwd_kv_chunks(int kb, int N, int H, bool causal) {
@@ -758,23 +758,26 @@ struct KvLayout {
     static constexpr int CHUNK = BRC * RW;        // halves per Q (or dO) chunk
     static constexpr int STAGE = 2 * CHUNK;       // Q and dO
     static constexpr int STATS = 2 * BRC;         // floats: lse2, D per row
+    static constexpr int CHUNK_BYTES = 2 * STAGE * 2;   // two stages
+    static constexpr int STATS_BYTES = 2 * STATS * 4;
+    static constexpr int LDS_BYTES = CHUNK_BYTES + STATS_BYTES + 2 * BRC * 4;
 };
 
 template <int DH, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_bwd_kv(FlashArgs p, float* part_ws, int parts_per_batch) {
+DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, int blk, char* lds) {
     using L = KvLayout<DH>;
     constexpr int KS = DH / 32, DB = DH / 16, RW = L::RW;
     constexpr int PIECES = BRC * DH / 8;              // 16-byte pieces of a chunk
     constexpr int PPT = (2 * PIECES + 255) / 256;     // per thread (Q and dO)
-    __shared__ __attribute__((aligned(16))) f16 chunk_s[2 * L::STAGE];
-    __shared__ __attribute__((aligned(16))) float stats_s[2 * L::STATS];
-    __shared__ __attribute__((aligned(16))) int pos_s[2 * BRC];  // position of each row
+    f16* chunk_s = reinterpret_cast<f16*>(lds);
+    float* stats_s = reinterpret_cast<float*>(lds + L::CHUNK_BYTES);
+    int* pos_s = reinterpret_cast<int*>(lds + L::CHUNK_BYTES + L::STATS_BYTES);  // position of each row
 
     const int H = p.H, N = p.N, NH = N * H;
     const int nkb = (N + BKB - 1) / BKB;
     // workgroup -> (batch, key block, part); heavy key blocks first
-    const int b = blockIdx.x / parts_per_batch;
-    int rem = blockIdx.x % parts_per_batch, kb = 0, nparts = 0, slot0 = 0;
+    const int b = blk / parts_per_batch;
+    int rem = blk % parts_per_batch, kb = 0, nparts = 0, slot0 = 0;
     for (; kb < nkb; ++kb) {
         nparts = bwd_kv_parts(kb, N, H, CAUSAL);
         if (rem < nparts) break;
@@ -1023,17 +1026,17 @@ struct DqLayout {
 };
 
 template <int DH, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
+DEV void bwd_q_body(const FlashArgs& p, int blk, char* lds) {
     using L = DqLayout<DH>;
     constexpr int KS = DH / 32, DB = DH / 16, KW = L::KW, OW = L::OW;
     constexpr int KPER = KC * DH / 8 / 64;  // 16-byte K pieces per lane
-    __shared__ __attribute__((aligned(16))) float smem_f[L::LDS_BYTES / 4];
+    float* smem_f = reinterpret_cast<float*>(lds);
     f16* kslot = reinterpret_cast<f16*>(smem_f) + (threadIdx.x >> 6) * L::KSLOT;
 
     const int H = p.H, N = p.N, NH = N * H;
     const int nrg = (NH + 63) / 64;
-    const int b = blockIdx.x % p.B;
-    const int rg = CAUSAL ? nrg - 1 - blockIdx.x / p.B : blockIdx.x / p.B;  // heavy rows first
+    const int b = blk % p.B;
+    const int rg = CAUSAL ? nrg - 1 - blk / p.B : blk / p.B;  // heavy rows first
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -1179,6 +1182,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_q(FlashArgs p) {
             *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
         }
     }
+}
+
+// dK/dV (key blocks x row parts) and dQ (row tiles) in one launch: the
+// first n_kv workgroups run the former, heavy key blocks first, the rest
+// the latter, heavy row tiles first.  The two halves are independent (both
+// read only Q, K, V, dO and the row statistics), so the dQ tiles fill the
+// CUs that the short dK/dV parts free.
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_bwd_kvq(FlashArgs p, float* part_ws, int parts_per_batch, int n_kv) {
+    constexpr int KVB = KvLayout<DH>::LDS_BYTES, QB = DqLayout<DH>::LDS_BYTES;
+    __shared__ __attribute__((aligned(16))) char lds[KVB > QB ? KVB : QB];
+    if ((int)blockIdx.x < n_kv) bwd_kv_body<DH, CAUSAL>(p, part_ws, parts_per_batch, blockIdx.x, lds);
+    else bwd_q_body<DH, CAUSAL>(p, blockIdx.x - n_kv, lds);
 }
 
 // lse2_rows / d_rows from a saved LSE and O: D_i = rowsum(dO_i * O_i).
@@ -1642,18 +1658,16 @@ hipError_t launch_bwd_split(const FlashArgs& a, bool causal, float* parts, int p
     const int NH = a.N * a.H;
     dim3 gp((unsigned)(((int64_t)a.B * NH * (DH / 8) + 255) / 256));
     hipLaunchKernelGGL(flash_bwd_pre<DH>, gp, dim3(256), 0, st, a);
-    dim3 gkv((unsigned)(a.B * parts_per_batch));
-    dim3 gq((unsigned)((NH + 63) / 64 * a.B));
+    const int n_kv = a.B * parts_per_batch;
+    dim3 gm((unsigned)(n_kv + (NH + 63) / 64 * a.B));
     const int nkb = (a.N + BKB - 1) / BKB;
     dim3 gr((unsigned)(a.B * nkb * 16));
     if (causal) {
-        hipLaunchKernelGGL((flash_bwd_kv<DH, true>), gkv, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_kvq<DH, true>), gm, dim3(256), 0, st, a, parts, parts_per_batch, n_kv);
         hipLaunchKernelGGL((flash_bwd_kv_reduce<DH, true>), gr, dim3(256), 0, st, a, parts, parts_per_batch);
-        hipLaunchKernelGGL((flash_bwd_q<DH, true>), gq, dim3(256), 0, st, a);
     } else {
-        hipLaunchKernelGGL((flash_bwd_kv<DH, false>), gkv, dim3(256), 0, st, a, parts, parts_per_batch);
+        hipLaunchKernelGGL((flash_bwd_kvq<DH, false>), gm, dim3(256), 0, st, a, parts, parts_per_batch, n_kv);
         hipLaunchKernelGGL((flash_bwd_kv_reduce<DH, false>), gr, dim3(256), 0, st, a, parts, parts_per_batch);
-        hipLaunchKernelGGL((flash_bwd_q<DH, false>), gq, dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
