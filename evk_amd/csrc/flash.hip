@@ -724,7 +724,8 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 // block, with K^T and V^T as B-operand registers for the whole kernel.  The
 // workgroup walks 32-row chunks of the flattened (position, head) query rows,
 // so the MQA sum over heads happens inside the MFMA accumulation.  A chunk
-// (Q and dO rows, lse2 and D) is staged once in LDS for all four waves:
+// (Q and dO rows, and per row the base-2 LSE and D = rowsum(dO * O), formed
+// while staging from the O rows) is staged once in LDS for all four waves:
 //   S = Q K^T, dP = dO V^T (16 rows x 16 keys per v_mfma_f32_16x16x32_f16,
 //       A = rows read from LDS): lane owns one key, 4 rows per 16-row block
 //   P = 2^(S*scale*log2e - lse2_row), dS = P (dP - D_row)
@@ -738,6 +739,14 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 // and flash_bwd_kv_reduce sums them in part order (deterministic).
 // ---------------------------------------------------------------------------
 typedef int intx4 __attribute__((ext_vector_type(4)));
+
+// fp32 sum of the 8 products of two fp16 vectors
+DEV float dot8(const half8& x, const half8& y) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)x[e], (float)y[e], acc);
+    return acc;
+}
 
 constexpr int BKB = 128;       // keys per workgroup (4 waves x 32)
 constexpr int BRC = 32;        // flattened query rows per chunk
@@ -820,9 +829,12 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
     // chunk staging: thread t moves 16-byte pieces t, t+256, ... of [Q rows | dO rows]
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
-    const __amdgpu_buffer_rsrc_t lres = buf_rsrc(p.lse2_rows + (int64_t)b * NH, (uint32_t)NH * 4);
-    const __amdgpu_buffer_rsrc_t dres = buf_rsrc(p.d_rows + (int64_t)b * NH, (uint32_t)NH * 4);
-    u32x4 pr[PPT];
+    const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
+    // A thread holds at most one dO piece (DH <= 64); with it the O piece at
+    // the same place, so that D = rowsum(dO * O) comes from the DH/8 lanes
+    // of a row.  Rows past NH read as zeros: D = 0, lse2 = 0 (their Q and
+    // dO rows are zero too, so they add nothing).
+    u32x4 pr[PPT], po = {0u, 0u, 0u, 0u};
     float sr = 0.0f;
     int spos = 0;
     auto gload = [&](int c) {
@@ -832,28 +844,41 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
             const int pc = threadIdx.x + 256 * i;
             const int which = pc / PIECES, pi = pc % PIECES;
             const uint32_t off = (row0 * DH + pi * 8) * 2;
-            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES)
+            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES) {
                 pr[i] = buf_load16(which ? gres : qres, off, 0);
+                if (which) po = buf_load16(ores, off, 0);
+            }
         }
-        if (threadIdx.x < 2 * BRC) {
-            const int which = threadIdx.x / BRC, r = threadIdx.x % BRC;
-            sr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(which ? dres : lres,
-                                                                                 (row0 + r) * 4, 0, 0));
-        } else if (threadIdx.x < 3 * BRC) {
-            spos = (int)((row0 + threadIdx.x - 2 * BRC) / (uint32_t)H);
+        if (threadIdx.x < BRC) {  // base-2 LSE of row row0 + t, from the (B, H, N) LSE
+            const uint32_t row = row0 + threadIdx.x;
+            sr = row < (uint32_t)NH ? p.lse[((int64_t)b * H + row % H) * N + row / H] * kLog2e : 0.0f;
+        } else if (threadIdx.x < 2 * BRC) {
+            spos = (int)((row0 + threadIdx.x - BRC) / (uint32_t)H);
         }
     };
     auto lstore = [&](int stage) {
         f16* cs = chunk_s + stage * L::STAGE;
+        float dsum = 0.0f;
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int pc = threadIdx.x + 256 * i;
             const int which = pc / PIECES, pi = pc % PIECES;
-            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES)
+            if (2 * PIECES % 256 == 0 || pc < 2 * PIECES) {
                 *reinterpret_cast<u32x4*>(cs + which * L::CHUNK + (pi / (DH / 8)) * RW + (pi % (DH / 8)) * 8) = pr[i];
+                if (which) dsum = dot8(as_half8(pr[i]), as_half8(po));
+            }
         }
-        if (threadIdx.x < 2 * BRC) stats_s[stage * L::STATS + threadIdx.x] = sr;
-        else if (threadIdx.x < 3 * BRC) pos_s[stage * BRC + threadIdx.x - 2 * BRC] = spos;
+#pragma unroll
+        for (int o = 1; o < DH / 8; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            const int pi = pc % PIECES;
+            if (pc >= PIECES && pc < 2 * PIECES && pi % (DH / 8) == 0)
+                stats_s[stage * L::STATS + BRC + pi / (DH / 8)] = dsum;
+        }
+        if (threadIdx.x < BRC) stats_s[stage * L::STATS + threadIdx.x] = sr;
+        else if (threadIdx.x < 2 * BRC) pos_s[stage * BRC + threadIdx.x - BRC] = spos;
     };
 
     if (c_lo < c_hi) {
@@ -988,8 +1013,18 @@ __global__ __launch_bounds__(256) void flash_bwd_kv_reduce(FlashArgs p, const fl
     if (nparts == 1) return;  // written directly by its only part
     for (int e = slice * 256 + threadIdx.x; e < SLOT; e += 16 * 256) {
         const floatx4* src = reinterpret_cast<const floatx4*>(part_ws) + ((int64_t)b * parts_per_batch + slot0) * SLOT + e;
+        // part order as written; loads go out 8 at a time so that their
+        // latencies overlap
         floatx4 acc = src[0];
-        for (int q = 1; q < nparts; ++q) acc += src[(int64_t)q * SLOT];
+        int q = 1;
+        for (; q + 8 <= nparts; q += 8) {
+            floatx4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(q + u) * SLOT];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; q < nparts; ++q) acc += src[(int64_t)q * SLOT];
         // e = ((wave * 2 + which) * 2 + k2) * DB + d) * 64 + lane
         const int lane = e % 64, d = (e / 64) % DB, k2 = (e / (64 * DB)) % 2, which = (e / (64 * DB * 2)) % 2,
                   wave = e / (64 * PW);
@@ -1052,8 +1087,11 @@ DEV void bwd_q_body(const FlashArgs& p, int blk, char* lds) {
     const uint32_t rows_bytes = (uint32_t)(last - R0 + 1) * DH * 2;
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, rows_bytes);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + ((int64_t)b * NH + R0) * DH, rows_bytes);
+    const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + ((int64_t)b * NH + R0) * DH, rows_bytes);
 
-    // B operands: row R0 + 16 qb + l16, dh [32 ks + 8 g, +8); row statistics
+    // B operands: row R0 + 16 qb + l16, dh [32 ks + 8 g, +8); row statistics:
+    // the base-2 LSE from the (B, H, N) LSE, and D = rowsum(dO * O) over the
+    // row's four lane groups
     half8 qf[4][KS], gf[4][KS];
     float l2[4], dd[4];
     int qpos[4];
@@ -1061,14 +1099,17 @@ DEV void bwd_q_body(const FlashArgs& p, int blk, char* lds) {
     for (int qb = 0; qb < 4; ++qb) {
         const int row = min(R0 + qb * 16 + l16, NH - 1);
         qpos[qb] = row / H;
-        l2[qb] = p.lse2_rows[(int64_t)b * NH + row];
-        dd[qb] = p.d_rows[(int64_t)b * NH + row];
+        l2[qb] = p.lse[((int64_t)b * H + row % H) * N + row / H] * kLog2e;
+        float dsum = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const uint32_t off = (uint32_t)((qb * 16 + l16) * DH + ks * 32 + g * 8) * 2;
             qf[qb][ks] = as_half8(buf_load16(qres, off, 0));
             gf[qb][ks] = as_half8(buf_load16(gres, off, 0));
+            dsum += dot8(gf[qb][ks], as_half8(buf_load16(ores, off, 0)));
         }
+        dsum += __shfl_xor(dsum, 16, 64);
+        dd[qb] = dsum + __shfl_xor(dsum, 32, 64);
     }
     floatx4 acc[DB][4];
 #pragma unroll
@@ -1656,8 +1697,6 @@ template <int DH>
 hipError_t launch_bwd_split(const FlashArgs& a, bool causal, float* parts, int parts_per_batch,
                             hipStream_t st) {
     const int NH = a.N * a.H;
-    dim3 gp((unsigned)(((int64_t)a.B * NH * (DH / 8) + 255) / 256));
-    hipLaunchKernelGGL(flash_bwd_pre<DH>, gp, dim3(256), 0, st, a);
     const int n_kv = a.B * parts_per_batch;
     dim3 gm((unsigned)(n_kv + (NH + 63) / 64 * a.B));
     const int nkb = (a.N + BKB - 1) / BKB;
@@ -1707,7 +1746,7 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
     int parts_per_batch = 0;
     if (split)
         for (int kb = 0; kb < nkb; ++kb) parts_per_batch += bwd_kv_parts(kb, a.N, a.H, causal);
-    const size_t stats_b = al(2 * rows * sizeof(float));
+    const size_t stats_b = split ? 0 : al(2 * rows * sizeof(float));  // split: formed in-kernel
     const size_t part_b = split ? al((size_t)a.B * parts_per_batch * 4 * (2 * 2 * (dh / 16)) * 64 * 16) : 0;
     const size_t fwd_b = (split && !have_lse) ? al(rows * dh * 2) + al(rows * sizeof(float)) : 0;
     const size_t need = stats_b + part_b + fwd_b;
@@ -1718,8 +1757,8 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
         EVK_HIP(hipMalloc(&g_bwd_ws, need));
         g_bwd_ws_bytes = need;
     }
-    a.lse2_rows = reinterpret_cast<float*>(g_bwd_ws);
-    a.d_rows = a.lse2_rows + rows;
+    a.lse2_rows = split ? nullptr : reinterpret_cast<float*>(g_bwd_ws);
+    a.d_rows = split ? nullptr : a.lse2_rows + rows;
     hipError_t e;
     if (split) {
         float* parts = reinterpret_cast<float*>(g_bwd_ws + stats_b);
