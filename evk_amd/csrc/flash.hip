@@ -454,7 +454,7 @@ struct KsLayout {
     static constexpr int VSLOT = KC * VW;        // halves per wave slot
     static constexpr int VPER = KC * DH / 8 / 64;  // 16-byte V pieces per lane
     static constexpr int OW = DH + 4;            // merge row stride (floats)
-    static constexpr int MERGE = 4 * ROWS * OW + 2 * 4 * ROWS + 2 * ROWS;  // O partials, m, l; m_tot, l_tot
+    static constexpr int MERGE = 4 * ROWS * OW + 2 * 4 * ROWS;  // O partials, m, l of the four waves
     static constexpr int LDS_BYTES = (MERGE * 4 > 4 * VSLOT * 2) ? MERGE * 4 : 4 * VSLOT * 2;
 };
 
@@ -649,8 +649,11 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     for (; c < nch; c += 4) chunk(c, std::true_type{});
 
     // ---- merge the four waves' partial softmax states ----
-    // Merge addresses derive from an opaque copy of the lane id, so the
-    // compiler computes them here instead of keeping them live through the loop.
+    // Each wave stores its state as it stands (m, l and O relative to its own
+    // running max); after one barrier the lanes that write a row combine the
+    // four with weights 2^(m_w - m).  Merge addresses derive from an opaque
+    // copy of the lane id, so the compiler computes them here instead of
+    // keeping them live through the loop.
     int ml = lane;
     asm volatile("" : "+v"(ml));
     const int ml16 = ml & 15, mg = ml >> 4;
@@ -658,36 +661,16 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     float* ob = smem_f;                          // [wave][ROWS][OW]
     float* mw = smem_f + 4 * ROWS * L::OW;       // [wave][ROWS]
     float* lw = mw + 4 * ROWS;                   // [wave][ROWS]
-    float* mt = lw + 4 * ROWS;                   // [ROWS]
-    float* lt = mt + ROWS;                       // [ROWS]
-    if (mg == 0) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            mw[wave * ROWS + qb * 16 + ml16] = m_ref[qb];
-            lw[wave * ROWS + qb * 16 + ml16] = lacc[qb][0];
-        }
-    }
-    __syncthreads();
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int q = qb * 16 + ml16;
-        float m = mw[q];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) m = fmaxf(m, mw[w * ROWS + q]);
-        const float mine = (m_ref[qb] == -INFINITY) ? 0.0f : fast_exp2(m_ref[qb] - m);
-        if (wave == 0 && mg == 0) {
-            float l = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float mwq = mw[w * ROWS + q];
-                l += (mwq == -INFINITY) ? 0.0f : fast_exp2(mwq - m) * lw[w * ROWS + q];
-            }
-            mt[q] = m;
-            lt[q] = l;
+        if (mg == 0) {
+            mw[wave * ROWS + q] = m_ref[qb];
+            lw[wave * ROWS + q] = lacc[qb][0];
         }
 #pragma unroll
         for (int d = 0; d < DB; ++d)
-            *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb] * mine;
+            *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb];
     }
     __syncthreads();
     // wave w finishes rows [w*ROWS/4, (w+1)*ROWS/4): a lane owns 8 dh of one row
@@ -696,21 +679,28 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         const int q = wave * RPW + rr;
         const int row = R0 + q;
         const int dc = (ml % CPR) * 8;
-        floatx4 a0 = *reinterpret_cast<const floatx4*>(ob + q * L::OW + dc);
-        floatx4 a1 = *reinterpret_cast<const floatx4*>(ob + q * L::OW + dc + 4);
+        float mv[4], m = -INFINITY;
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            a0 += *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc);
-            a1 += *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc + 4);
+        for (int w = 0; w < 4; ++w) {
+            mv[w] = mw[w * ROWS + q];
+            m = fmaxf(m, mv[w]);
         }
-        const float l = lt[q];
+        floatx4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float sc = mv[w] == -INFINITY ? 0.0f : fast_exp2(mv[w] - m);
+            l += sc * lw[w * ROWS + q];
+            a0 += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc);
+            a1 += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc + 4);
+        }
         const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
         if (active && row < NH) {
             u32x4 o = {pack_h2(a0[0] * inv_l, a0[1] * inv_l), pack_h2(a0[2] * inv_l, a0[3] * inv_l),
                        pack_h2(a1[0] * inv_l, a1[1] * inv_l), pack_h2(a1[2] * inv_l, a1[3] * inv_l)};
             *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
             if (p.lse && dc == 0) {
-                const float lse = l > 0.0f ? (mt[q] + log2f(l)) * kLn2 : -INFINITY;
+                const float lse = l > 0.0f ? (m + log2f(l)) * kLn2 : -INFINITY;
                 p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
             }
         }
