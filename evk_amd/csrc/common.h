@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "../../include/evkhip.h"
 
 typedef _Float16 f16;
@@ -96,6 +99,16 @@ DEV half4 lds_read_tr(const f16* p) {
     fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
         (__attribute__((address_space(3))) fp16x4_t*)(p));
     return __builtin_bit_cast(half4, v);
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <class F, int... S>
+DEV void static_for_impl(F&& f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, class F>
+DEV void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 DEV half8 cat4(const half4& a, const half4& b) {

@@ -284,16 +284,6 @@ DEV half8 frag_t(const f16* t, int k0, int c0, int g, int trow, int tcol) {
     return cat4(lds_read_tr(at(k)), lds_read_tr(at(k + 4)));
 }
 
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
-template <class F, int... S>
-DEV void static_for_impl(F&& f, std::integer_sequence<int, S...>) {
-    (f(std::integral_constant<int, S>{}), ...);
-}
-template <int N, class F>
-DEV void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 DEV int xcd_tile(int w, int total) {
     if (total % 8) return w;
     return (w % 8) * (total / 8) + w / 8;  // XCD w%8 gets a contiguous range

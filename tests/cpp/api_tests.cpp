@@ -178,6 +178,32 @@ static void test_matmul() {
     TEST(off);
 }
 
+// Host I/O batched under one submit: uploads, an op and a download recorded
+// with submit=false (evk_ai.h:279-294), then a single SubmitCmd(true).  Twice,
+// so that the second round's uploads follow the first round's download.
+static void test_batched_host_io() {
+    std::printf("test_batched_host_io()\n");
+    const uint32_t n = 64;
+    Tensor a({n, n}), b({n, n}), c({n, n});
+    for (int round = 0; round < 2; ++round) {
+        float16_t* ha = a.cpu();
+        float16_t* hb = b.cpu();
+        for (uint32_t i = 0; i < n * n; ++i) {
+            ha[i] = float16_t(i / n == i % n ? float(round + 2) : 0.0f);  // (round+2) I
+            hb[i] = float16_t(float((i * 7 + round) % 13) - 6.0f);       // small integers
+        }
+        a.cpu_upload(false);
+        b.cpu_upload(false);
+        evk::ai::matmul(a, b, c);
+        c.cpu_download(false);
+        evk::ai::SubmitCmd(true);
+        bool ok = true;
+        for (uint32_t i = 0; i < n * n; ++i)
+            ok &= float(c.cpu()[i]) == float(round + 2) * (float((i * 7 + round) % 13) - 6.0f);
+        TEST(ok);
+    }
+}
+
 static void test_matmul_broadcast() {
     std::printf("test_matmul_broadcast()\n");
     Tensor a({1, 32, 32}), b({32, 32}), c({3, 32, 32});
@@ -609,6 +635,7 @@ int main(int argc, char** argv) {
     test_runtime_commands();
     test_add();
     test_matmul();
+    test_batched_host_io();
     test_matmul_broadcast();
     test_matmul_vs_cpu();
     test_flash_attention_vs_cpu();
