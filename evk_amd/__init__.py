@@ -74,6 +74,25 @@ SIGNATURES = {
     "evkhip_add": (C.c_int, [TP, TP, TP, C.c_void_p]),
     "evkhip_embed": (C.c_int, [TP, TP, TP, C.c_void_p]),
     "evkhip_greedy_sample": (C.c_int, [TP, TP, C.c_uint32, C.c_uint16, C.c_uint16, C.c_void_p]),
+    "evkhip_scale": (C.c_int, [TP, C.c_float, C.c_void_p]),
+    "evkhip_relu": (C.c_int, [TP, TP, C.c_void_p]),
+    "evkhip_relu_backward": (C.c_int, [TP, TP, TP, C.c_void_p]),
+    "evkhip_gelu_backward": (C.c_int, [TP, TP, TP, C.c_void_p]),
+    "evkhip_mse_loss": (C.c_int, [TP, TP, TP, TP, C.c_void_p]),
+    "evkhip_sgd": (C.c_int, [TP, TP, C.c_float, C.c_void_p]),
+    "evkhip_adam": (C.c_int, [TP, TP, TP, TP] + [C.c_float] * 6 + [C.c_void_p]),
+    "evkhip_softmax": (C.c_int, [TP, TP, C.c_float, C.c_void_p]),
+    "evkhip_softmax_backward": (C.c_int, [TP, TP, TP, C.c_float, C.c_void_p]),
+    "evkhip_rms_norm_backward": (C.c_int, [TP, TP, TP, C.c_float, C.c_void_p]),
+    "evkhip_cross_entropy_loss": (C.c_int, [TP, TP, TP, TP, C.c_void_p]),
+    "evkhip_sum_batch": (C.c_int, [TP, TP, C.c_uint32, C.c_uint32, C.c_void_p]),
+    "evkhip_apply_causal_mask": (C.c_int, [TP, C.c_void_p]),
+    "evkhip_position_add": (C.c_int, [TP, TP, TP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p]),
+    "evkhip_position_add_backward": (C.c_int, [TP, TP, TP, C.c_uint32, C.c_uint32, C.c_uint32,
+                                               C.c_void_p]),
+    "evkhip_rope_backward": (C.c_int, [TP, TP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float,
+                                       C.c_void_p]),
+    "evkhip_embed_backward": (C.c_int, [TP, TP, TP, C.c_void_p]),
     "evkhip_model_weight_elems": (C.c_uint64, [C.POINTER(ModelCfg)]),
     "evkhip_model_cache_elems": (C.c_uint64, [C.POINTER(ModelCfg)]),
     "evkhip_model_prefill": (C.c_int, [C.POINTER(ModelCfg), C.c_void_p, C.c_void_p, C.c_void_p,
@@ -221,6 +240,104 @@ def embed(embeddings, indices, out, stream=None):
     _check(lib().evkhip_embed(_ref(desc(embeddings)), _ref(desc(indices)), _ref(desc(out)),
                               _stream(stream)))
     return out
+
+
+# ---- training ops (evk_ai.h:507-614); *_backward accumulate into grad_in ----
+
+def _D(t):
+    return _ref(desc(t))
+
+
+def scale(t, factor, stream=None):
+    _check(lib().evkhip_scale(_D(t), float(factor), _stream(stream)))
+    return t
+
+
+def relu(inp, out, stream=None):
+    _check(lib().evkhip_relu(_D(inp), _D(out), _stream(stream)))
+    return out
+
+
+def relu_backward(grad_out, inp, grad_in, stream=None):
+    _check(lib().evkhip_relu_backward(_D(grad_out), _D(inp), _D(grad_in), _stream(stream)))
+    return grad_in
+
+
+def gelu_backward(grad_out, inp, grad_in, stream=None):
+    _check(lib().evkhip_gelu_backward(_D(grad_out), _D(inp), _D(grad_in), _stream(stream)))
+    return grad_in
+
+
+def mse_loss(predicted, target, pred_grad, result, stream=None):
+    _check(lib().evkhip_mse_loss(_D(predicted), _D(target), _D(pred_grad), _D(result), _stream(stream)))
+    return result
+
+
+def sgd(param, gradient, learning_rate, stream=None):
+    _check(lib().evkhip_sgd(_D(param), _D(gradient), float(learning_rate), _stream(stream)))
+    return param
+
+
+def adam(param, gradient, m_state, v_state, learning_rate, beta1, beta2, beta1_correction_inv,
+         beta2_correction_inv, epsilon, stream=None):
+    _check(lib().evkhip_adam(_D(param), _D(gradient), _D(m_state), _D(v_state), float(learning_rate),
+                             float(beta1), float(beta2), float(beta1_correction_inv),
+                             float(beta2_correction_inv), float(epsilon), _stream(stream)))
+    return param
+
+
+def softmax(inp, out, input_scale=1.0, stream=None):
+    _check(lib().evkhip_softmax(_D(inp), _D(out), float(input_scale), _stream(stream)))
+    return out
+
+
+def softmax_backward(probs, grad_out, grad_in, scale=1.0, stream=None):
+    _check(lib().evkhip_softmax_backward(_D(probs), _D(grad_out), _D(grad_in), float(scale),
+                                         _stream(stream)))
+    return grad_in
+
+
+def rms_norm_backward(inp, grad_out, grad_in, eps=1e-4, stream=None):
+    _check(lib().evkhip_rms_norm_backward(_D(inp), _D(grad_out), _D(grad_in), float(eps), _stream(stream)))
+    return grad_in
+
+
+def cross_entropy_loss(logits, targets, grad, result, stream=None):
+    _check(lib().evkhip_cross_entropy_loss(_D(logits), _D(targets), _D(grad), _D(result), _stream(stream)))
+    return result
+
+
+def sum_batch(inp, out, batch_count, size_per_batch, stream=None):
+    _check(lib().evkhip_sum_batch(_D(inp), _D(out), int(batch_count), int(size_per_batch), _stream(stream)))
+    return out
+
+
+def apply_causal_mask(scores, stream=None):
+    _check(lib().evkhip_apply_causal_mask(_D(scores), _stream(stream)))
+    return scores
+
+
+def position_add(inp, pos_emb, out, batch_size, seq_len, embed_dim, stream=None):
+    _check(lib().evkhip_position_add(_D(inp), _D(pos_emb), _D(out), int(batch_size), int(seq_len),
+                                     int(embed_dim), _stream(stream)))
+    return out
+
+
+def position_add_backward(grad_out, grad_in, grad_pos, batch_size, seq_len, embed_dim, stream=None):
+    _check(lib().evkhip_position_add_backward(_D(grad_out), _D(grad_in), _D(grad_pos), int(batch_size),
+                                              int(seq_len), int(embed_dim), _stream(stream)))
+    return grad_in, grad_pos
+
+
+def rope_backward(grad_out, grad_in, batch_size, seq_len, embed_dim, rotary_base=10000.0, stream=None):
+    _check(lib().evkhip_rope_backward(_D(grad_out), _D(grad_in), int(batch_size), int(seq_len),
+                                      int(embed_dim), float(rotary_base), _stream(stream)))
+    return grad_in
+
+
+def embed_backward(grad_out, indices, grad_embeddings, stream=None):
+    _check(lib().evkhip_embed_backward(_D(grad_out), _D(indices), _D(grad_embeddings), _stream(stream)))
+    return grad_embeddings
 
 
 def greedy_sample(logits, out_tokens, position, token_base, token_count, stream=None):

@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
 
 namespace evkhip {
 
@@ -90,6 +91,7 @@ int evkhip_shutdown(void) {
     flash_free_workspace();
     decode_ops_free_workspace();
     model_free_workspace();
+    train_ops_free_workspace();
     return EVKHIP_OK;
 }
 
@@ -313,6 +315,208 @@ int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out_t
                   "greedy_sample: token range exceeds vocab");
     return greedy_launch((const f16*)logits->data, (uint16_t*)out_tokens->data, (int)B, (int)S, (int)V,
                          (int)position, token_base, token_count, as_stream(stream));
+}
+
+// ---- training ops ----
+
+static bool all_aligned(std::initializer_list<const evkhip_tensor*> ts) {
+    for (const evkhip_tensor* x : ts)
+        if (!aligned16(x->data)) return false;
+    return true;
+}
+
+int evkhip_scale(const evkhip_tensor* t, float factor, void* stream) {
+    CHECK(check_tensor(t, "scale: tensor", 1, EVKHIP_MAX_DIMS));
+    return scale_launch((f16*)t->data, factor, (int64_t)numel(t), all_aligned({t}), as_stream(stream));
+}
+
+int evkhip_relu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream) {
+    CHECK(check_tensor(in, "relu: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "relu: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(in, out), EVKHIP_ERR_SHAPE, "relu: shapes differ");
+    return relu_launch((const f16*)in->data, (f16*)out->data, (int64_t)numel(in), all_aligned({in, out}),
+                       as_stream(stream));
+}
+
+int evkhip_relu_backward(const evkhip_tensor* grad_out, const evkhip_tensor* in, const evkhip_tensor* grad_in,
+                         void* stream) {
+    CHECK(check_tensor(grad_out, "relu_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(in, "relu_backward: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "relu_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    const uint64_t n = numel(in);
+    EVK_RETURN_IF(numel(grad_out) != n || numel(grad_in) != n, EVKHIP_ERR_SHAPE,
+                  "relu_backward: element counts differ");
+    return relu_bwd_launch((const f16*)grad_out->data, (const f16*)in->data, (f16*)grad_in->data, (int64_t)n,
+                           all_aligned({grad_out, in, grad_in}), as_stream(stream));
+}
+
+int evkhip_gelu_backward(const evkhip_tensor* grad_out, const evkhip_tensor* in, const evkhip_tensor* grad_in,
+                         void* stream) {
+    CHECK(check_tensor(grad_out, "gelu_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(in, "gelu_backward: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "gelu_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    const uint64_t n = numel(in);
+    EVK_RETURN_IF(numel(grad_out) != n || numel(grad_in) != n, EVKHIP_ERR_SHAPE,
+                  "gelu_backward: element counts differ");
+    return gelu_bwd_launch((const f16*)grad_out->data, (const f16*)in->data, (f16*)grad_in->data, (int64_t)n,
+                           all_aligned({grad_out, in, grad_in}), as_stream(stream));
+}
+
+int evkhip_mse_loss(const evkhip_tensor* predicted, const evkhip_tensor* target, const evkhip_tensor* pred_grad,
+                    const evkhip_tensor* result, void* stream) {
+    CHECK(check_tensor(predicted, "mse_loss: predicted", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(target, "mse_loss: target", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(pred_grad, "mse_loss: pred_grad", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(result, "mse_loss: result", 1, 1));
+    EVK_RETURN_IF(!same_shape(predicted, target), EVKHIP_ERR_SHAPE, "mse_loss: predicted and target differ");
+    EVK_RETURN_IF(numel(pred_grad) != numel(predicted), EVKHIP_ERR_SHAPE, "mse_loss: pred_grad size");
+    EVK_RETURN_IF(result->dims[0] < 1, EVKHIP_ERR_SHAPE, "mse_loss: result must hold one value");
+    return mse_loss_launch((const f16*)predicted->data, (const f16*)target->data, (f16*)pred_grad->data,
+                           (f16*)result->data, (int64_t)numel(predicted), as_stream(stream));
+}
+
+int evkhip_sgd(const evkhip_tensor* param, const evkhip_tensor* gradient, float learning_rate, void* stream) {
+    CHECK(check_tensor(param, "sgd: param", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(gradient, "sgd: gradient", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(param, gradient), EVKHIP_ERR_SHAPE, "sgd: param and gradient differ");
+    return sgd_launch((f16*)param->data, (const f16*)gradient->data, learning_rate, (int64_t)numel(param),
+                      all_aligned({param, gradient}), as_stream(stream));
+}
+
+int evkhip_adam(const evkhip_tensor* param, const evkhip_tensor* gradient, const evkhip_tensor* m_state,
+                const evkhip_tensor* v_state, float learning_rate, float beta1, float beta2,
+                float beta1_correction_inv, float beta2_correction_inv, float epsilon, void* stream) {
+    CHECK(check_tensor(param, "adam: param", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(gradient, "adam: gradient", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(m_state, "adam: m_state", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(v_state, "adam: v_state", 1, EVKHIP_MAX_DIMS));
+    const uint64_t n = numel(param);
+    EVK_RETURN_IF(!same_shape(param, gradient), EVKHIP_ERR_SHAPE, "adam: param and gradient differ");
+    EVK_RETURN_IF(numel(m_state) != n || numel(v_state) != n, EVKHIP_ERR_SHAPE,
+                  "adam: state must hold one value per parameter");
+    return adam_launch((f16*)param->data, (const f16*)gradient->data, (f16*)m_state->data, (f16*)v_state->data,
+                       (int64_t)n, learning_rate, beta1, beta2, beta1_correction_inv, beta2_correction_inv, epsilon,
+                       as_stream(stream));
+}
+
+int evkhip_softmax(const evkhip_tensor* in, const evkhip_tensor* out, float input_scale, void* stream) {
+    CHECK(check_tensor(in, "softmax: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "softmax: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(in, out), EVKHIP_ERR_SHAPE, "softmax: shapes differ");
+    const uint32_t D = dim_at(in, -1);
+    if (D == 0) return EVKHIP_OK;
+    return softmax_launch((const f16*)in->data, (f16*)out->data, input_scale, (int)D, (int64_t)(numel(in) / D),
+                          as_stream(stream));
+}
+
+int evkhip_softmax_backward(const evkhip_tensor* probs, const evkhip_tensor* grad_out,
+                            const evkhip_tensor* grad_in, float scale, void* stream) {
+    CHECK(check_tensor(probs, "softmax_backward: probs", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_out, "softmax_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "softmax_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(probs, grad_out) || !same_shape(probs, grad_in), EVKHIP_ERR_SHAPE,
+                  "softmax_backward: shapes differ");
+    const uint32_t D = dim_at(probs, -1);
+    if (D == 0) return EVKHIP_OK;
+    return softmax_bwd_launch((const f16*)probs->data, (const f16*)grad_out->data, (f16*)grad_in->data, scale,
+                              (int)D, (int64_t)(numel(probs) / D), as_stream(stream));
+}
+
+int evkhip_rms_norm_backward(const evkhip_tensor* in, const evkhip_tensor* grad_out,
+                             const evkhip_tensor* grad_in, float eps, void* stream) {
+    CHECK(check_tensor(in, "rms_norm_backward: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_out, "rms_norm_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "rms_norm_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(!same_shape(in, grad_out) || !same_shape(in, grad_in), EVKHIP_ERR_SHAPE,
+                  "rms_norm_backward: shapes differ");
+    const uint32_t D = dim_at(in, -1);
+    if (D == 0) return EVKHIP_OK;
+    return rms_norm_bwd_launch((const f16*)in->data, (const f16*)grad_out->data, (f16*)grad_in->data, eps, (int)D,
+                               (int64_t)(numel(in) / D), as_stream(stream));
+}
+
+int evkhip_cross_entropy_loss(const evkhip_tensor* logits, const evkhip_tensor* targets,
+                              const evkhip_tensor* grad, const evkhip_tensor* result, void* stream) {
+    CHECK(check_tensor(logits, "cross_entropy_loss: logits", 2, 2));
+    CHECK(check_tensor(targets, "cross_entropy_loss: targets", 1, 1));
+    CHECK(check_tensor(grad, "cross_entropy_loss: grad", 2, 2));
+    CHECK(check_tensor(result, "cross_entropy_loss: result", 1, 1));
+    const uint32_t P = logits->dims[0], V = logits->dims[1];
+    EVK_RETURN_IF(targets->dims[0] != P, EVKHIP_ERR_SHAPE, "cross_entropy_loss: targets must be (positions)");
+    EVK_RETURN_IF(!same_shape(logits, grad), EVKHIP_ERR_SHAPE, "cross_entropy_loss: grad must match logits");
+    EVK_RETURN_IF(result->dims[0] != 1, EVKHIP_ERR_SHAPE, "cross_entropy_loss: result must be (1)");
+    EVK_RETURN_IF(V == 0 && P > 0, EVKHIP_ERR_SHAPE, "cross_entropy_loss: empty vocabulary");
+    return cross_entropy_launch((const f16*)logits->data, (const uint16_t*)targets->data, (f16*)grad->data,
+                                (f16*)result->data, (int64_t)P, (int)V, as_stream(stream));
+}
+
+int evkhip_sum_batch(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t batch_count,
+                     uint32_t size_per_batch, void* stream) {
+    CHECK(check_tensor(in, "sum_batch: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "sum_batch: out", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(numel(in) < (uint64_t)batch_count * size_per_batch || numel(out) < size_per_batch,
+                  EVKHIP_ERR_SHAPE, "sum_batch: tensors hold fewer than batch_count*size_per_batch values");
+    return sum_batch_launch((const f16*)in->data, (f16*)out->data, (int)batch_count, (int64_t)size_per_batch,
+                            as_stream(stream));
+}
+
+int evkhip_apply_causal_mask(const evkhip_tensor* scores, void* stream) {
+    CHECK(check_tensor(scores, "apply_causal_mask: scores", 2, EVKHIP_MAX_DIMS));
+    const uint32_t N = dim_at(scores, -1);
+    EVK_RETURN_IF(dim_at(scores, -2) != N, EVKHIP_ERR_SHAPE, "apply_causal_mask: scores must be (..., N, N)");
+    if (N == 0) return EVKHIP_OK;
+    return causal_mask_launch((f16*)scores->data, (int64_t)(numel(scores) / ((uint64_t)N * N)), (int)N,
+                              as_stream(stream));
+}
+
+int evkhip_position_add(const evkhip_tensor* in, const evkhip_tensor* pos_emb, const evkhip_tensor* out,
+                        uint32_t batch_size, uint32_t seq_len, uint32_t embed_dim, void* stream) {
+    CHECK(check_tensor(in, "position_add: in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(pos_emb, "position_add: pos_emb", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(out, "position_add: out", 1, EVKHIP_MAX_DIMS));
+    const uint64_t per = (uint64_t)seq_len * embed_dim, n = per * batch_size;
+    EVK_RETURN_IF(numel(in) < n || numel(out) < n || numel(pos_emb) < per, EVKHIP_ERR_SHAPE,
+                  "position_add: tensors hold fewer than B*N*D (pos_emb N*D) values");
+    return position_add_launch((const f16*)in->data, (const f16*)pos_emb->data, (f16*)out->data, (int)batch_size,
+                               (int64_t)per, as_stream(stream));
+}
+
+int evkhip_position_add_backward(const evkhip_tensor* grad_out, const evkhip_tensor* grad_in,
+                                 const evkhip_tensor* grad_pos, uint32_t batch_size, uint32_t seq_len,
+                                 uint32_t embed_dim, void* stream) {
+    CHECK(check_tensor(grad_out, "position_add_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "position_add_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_pos, "position_add_backward: grad_pos", 1, EVKHIP_MAX_DIMS));
+    const uint64_t per = (uint64_t)seq_len * embed_dim, n = per * batch_size;
+    EVK_RETURN_IF(numel(grad_out) < n || numel(grad_in) < n || numel(grad_pos) < per, EVKHIP_ERR_SHAPE,
+                  "position_add_backward: tensors hold fewer than B*N*D (grad_pos N*D) values");
+    return position_add_bwd_launch((const f16*)grad_out->data, (f16*)grad_in->data, (f16*)grad_pos->data,
+                                   (int)batch_size, (int64_t)per, as_stream(stream));
+}
+
+int evkhip_rope_backward(const evkhip_tensor* grad_out, const evkhip_tensor* grad_in, uint32_t batch_size,
+                         uint32_t seq_len, uint32_t embed_dim, float rotary_base, void* stream) {
+    CHECK(check_tensor(grad_out, "rope_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_in, "rope_backward: grad_in", 1, EVKHIP_MAX_DIMS));
+    EVK_RETURN_IF(embed_dim % 2, EVKHIP_ERR_SHAPE, "rope_backward: embed_dim %u must be even", embed_dim);
+    const uint64_t n = (uint64_t)batch_size * seq_len * embed_dim;
+    EVK_RETURN_IF(numel(grad_out) < n || numel(grad_in) < n, EVKHIP_ERR_SHAPE,
+                  "rope_backward: tensors hold fewer than B*S*D values");
+    return rope_bwd_launch((const f16*)grad_out->data, (f16*)grad_in->data, (int)batch_size, (int)seq_len,
+                           (int)embed_dim, rotary_base, as_stream(stream));
+}
+
+int evkhip_embed_backward(const evkhip_tensor* grad_out, const evkhip_tensor* indices,
+                          const evkhip_tensor* grad_embeddings, void* stream) {
+    CHECK(check_tensor(grad_out, "embed_backward: grad_out", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(indices, "embed_backward: indices", 1, EVKHIP_MAX_DIMS));
+    CHECK(check_tensor(grad_embeddings, "embed_backward: grad_embeddings", 2, 2));
+    const uint32_t vocab = grad_embeddings->dims[0], dim = grad_embeddings->dims[1];
+    const uint64_t n_idx = numel(indices);
+    EVK_RETURN_IF(numel(grad_out) != n_idx * dim, EVKHIP_ERR_SHAPE,
+                  "embed_backward: grad_out must hold indices*embed_dim values");
+    return embed_bwd_launch((const f16*)grad_out->data, (const uint16_t*)indices->data, (f16*)grad_embeddings->data,
+                            (int64_t)n_idx, (int)dim, (int)vocab, as_stream(stream));
 }
 
 }  // extern "C"

@@ -51,6 +51,30 @@ int greedy_launch(const f16* logits, uint16_t* out, int B, int S, int V, int pos
                   int token_count, hipStream_t st);
 void decode_ops_free_workspace();
 
+// ---- train_ops.hip (vec: the caller's pointers are 16-byte aligned) ----
+int scale_launch(f16* x, float s, int64_t n, bool vec, hipStream_t st);
+int relu_launch(const f16* in, f16* out, int64_t n, bool vec, hipStream_t st);
+int relu_bwd_launch(const f16* gout, const f16* in, f16* gin, int64_t n, bool vec, hipStream_t st);
+int gelu_bwd_launch(const f16* gout, const f16* in, f16* gin, int64_t n, bool vec, hipStream_t st);
+int sgd_launch(f16* param, const f16* grad, float lr, int64_t n, bool vec, hipStream_t st);
+int adam_launch(f16* param, const f16* grad, f16* m, f16* v, int64_t n, float lr, float beta1, float beta2,
+                float c1inv, float c2inv, float eps, hipStream_t st);
+int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, hipStream_t st);
+int softmax_bwd_launch(const f16* probs, const f16* gout, f16* gin, float scale, int D, int64_t rows,
+                       hipStream_t st);
+int rms_norm_bwd_launch(const f16* in, const f16* gout, f16* gin, float eps, int D, int64_t rows, hipStream_t st);
+int mse_loss_launch(const f16* pred, const f16* tgt, f16* grad, f16* result, int64_t n, hipStream_t st);
+int cross_entropy_launch(const f16* logits, const uint16_t* tgt, f16* grad, f16* result, int64_t rows, int V,
+                         hipStream_t st);
+int sum_batch_launch(const f16* in, f16* out, int batch, int64_t per_batch, hipStream_t st);
+int causal_mask_launch(f16* scores, int64_t batch, int N, hipStream_t st);
+int position_add_launch(const f16* in, const f16* pos, f16* out, int B, int64_t per_batch, hipStream_t st);
+int position_add_bwd_launch(const f16* gout, f16* gin, f16* gpos, int B, int64_t per_batch, hipStream_t st);
+int rope_bwd_launch(const f16* gout, f16* gin, int B, int S, int E, float base, hipStream_t st);
+int embed_bwd_launch(const f16* gout, const uint16_t* idx, f16* gemb, int64_t n_idx, int dim, int vocab,
+                     hipStream_t st);
+void train_ops_free_workspace();
+
 // ---- model.hip ----
 void model_free_workspace();
 

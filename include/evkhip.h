@@ -133,6 +133,103 @@ int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out_t
                          void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Training ops: what the reference's Graph (evk_ai.h:616-1074) runs besides
+ * matmul and flash attention.  Gradient outputs that the shader accumulates
+ * into (grad_in += ...) are accumulated here too; every stored value is
+ * rounded to fp16 as the shader rounds it.
+ * ------------------------------------------------------------------------- */
+
+/* evk::ai::scale (evk_ai.h:599, evk_ai.cpp:992-1007, scale.comp): in place,
+ * t = t * factor. */
+int evkhip_scale(const evkhip_tensor* t, float factor, void* stream);
+
+/* evk::ai::relu (evk_ai.h:533, evk_ai.cpp:636-656, relu.comp). */
+int evkhip_relu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream);
+
+/* evk::ai::relu_backward (evk_ai.h:536, evk_ai.cpp:658-677, relu_bwd.comp):
+ * grad_in += (in > 0 ? grad_out : 0). */
+int evkhip_relu_backward(const evkhip_tensor* grad_out, const evkhip_tensor* in, const evkhip_tensor* grad_in,
+                         void* stream);
+
+/* evk::ai::gelu_backward (evk_ai.h:543, evk_ai.cpp:701-720, gelu_bwd.comp):
+ * grad_in += grad_out * d gelu(in) / d in (tanh form). */
+int evkhip_gelu_backward(const evkhip_tensor* grad_out, const evkhip_tensor* in, const evkhip_tensor* grad_in,
+                         void* stream);
+
+/* evk::ai::mse_loss (evk_ai.h:507, evk_ai.cpp:475-497, mse_loss.comp):
+ * result[0] = mean((p - t)^2), pred_grad = 2 (p - t) / n. */
+int evkhip_mse_loss(const evkhip_tensor* predicted, const evkhip_tensor* target, const evkhip_tensor* pred_grad,
+                    const evkhip_tensor* result, void* stream);
+
+/* evk::ai::sgd (evk_ai.h:510, evk_ai.cpp:499-519, sgd.comp):
+ * param -= learning_rate * gradient. */
+int evkhip_sgd(const evkhip_tensor* param, const evkhip_tensor* gradient, float learning_rate, void* stream);
+
+/* evk::ai::adam (evk_ai.h:514-518, evk_ai.cpp:521-566, adam.comp): one step
+ * with the caller's bias corrections 1/(1-beta1^t), 1/(1-beta2^t).  State
+ * (same element count as param, fp16): m_state = m / rms and v_state =
+ * log2(rms) + 41 (0 = rms 0), as the shader keeps them; zero-initialised
+ * state is a fresh optimiser. */
+int evkhip_adam(const evkhip_tensor* param, const evkhip_tensor* gradient, const evkhip_tensor* m_state,
+                const evkhip_tensor* v_state, float learning_rate, float beta1, float beta2,
+                float beta1_correction_inv, float beta2_correction_inv, float epsilon, void* stream);
+
+/* evk::ai::softmax (evk_ai.h:525, evk_ai.cpp:593-613, softmax.comp): over
+ * the last dimension of in * input_scale; entries <= -65504 are masked out
+ * (probability 0). */
+int evkhip_softmax(const evkhip_tensor* in, const evkhip_tensor* out, float input_scale, void* stream);
+
+/* evk::ai::softmax_backward (evk_ai.h:529, evk_ai.cpp:615-634,
+ * softmax_bwd.comp): grad_in += probs * (grad_out - dot(grad_out, probs)) * scale
+ * per row of the last dimension. */
+int evkhip_softmax_backward(const evkhip_tensor* probs, const evkhip_tensor* grad_out,
+                            const evkhip_tensor* grad_in, float scale, void* stream);
+
+/* evk::ai::rms_norm_backward (evk_ai.h:614, evk_ai.cpp:1072-1093,
+ * rms_norm_bwd.comp): grad_in += (g - y dot(g, y) / D) / rms per row. */
+int evkhip_rms_norm_backward(const evkhip_tensor* in, const evkhip_tensor* grad_out,
+                             const evkhip_tensor* grad_in, float eps, void* stream);
+
+/* evk::ai::cross_entropy_loss (evk_ai.h:552, evk_ai.cpp:722-780,
+ * cross_entropy*.comp): logits (P,V), targets (P) raw uint16; target 0 or
+ * >= V is ignored.  grad = (softmax - onehot) / n_valid (zero rows for
+ * ignored targets); result[0] = mean loss over valid rows (0 if none).  The
+ * per-row losses are summed in row order (deterministic). */
+int evkhip_cross_entropy_loss(const evkhip_tensor* logits, const evkhip_tensor* targets,
+                              const evkhip_tensor* grad, const evkhip_tensor* result, void* stream);
+
+/* evk::ai::sum_batch (evk_ai.h:605, evk_ai.cpp:1027-1041, sum_batch.comp):
+ * out[i] += sum_b in[b * size_per_batch + i]. */
+int evkhip_sum_batch(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t batch_count,
+                     uint32_t size_per_batch, void* stream);
+
+/* evk::ai::apply_causal_mask (evk_ai.h:577, evk_ai.cpp:862-882,
+ * causal_mask.comp): scores (..., N, N), entries j > i set to -65504. */
+int evkhip_apply_causal_mask(const evkhip_tensor* scores, void* stream);
+
+/* evk::ai::position_add (evk_ai.h:580-581, evk_ai.cpp:885-905,
+ * position_add.comp): out[b,t,:] = in[b,t,:] + pos_emb[t,:]. */
+int evkhip_position_add(const evkhip_tensor* in, const evkhip_tensor* pos_emb, const evkhip_tensor* out,
+                        uint32_t batch_size, uint32_t seq_len, uint32_t embed_dim, void* stream);
+
+/* evk::ai::position_add_backward (evk_ai.h:584-585, evk_ai.cpp:907-943,
+ * position_add_bwd.comp): grad_in += grad_out; grad_pos[t,:] += sum_b grad_out[b,t,:]. */
+int evkhip_position_add_backward(const evkhip_tensor* grad_out, const evkhip_tensor* grad_in,
+                                 const evkhip_tensor* grad_pos, uint32_t batch_size, uint32_t seq_len,
+                                 uint32_t embed_dim, void* stream);
+
+/* evk::ai::rope_backward (evk_ai.h:594-596, evk_ai.cpp:968-989, rope_bwd.comp):
+ * grad_in += the transposed rotation of grad_out (positions from 0). */
+int evkhip_rope_backward(const evkhip_tensor* grad_out, const evkhip_tensor* grad_in, uint32_t batch_size,
+                         uint32_t seq_len, uint32_t embed_dim, float rotary_base, void* stream);
+
+/* evk::ai::embed_backward (evk_ai.h:572, evk_ai.cpp:839-860, embed_bwd.comp):
+ * grad_embeddings[idx[r]] += grad_out[r] for r in order (the shader's
+ * sequence of fp16 roundings); ids >= vocab are skipped. */
+int evkhip_embed_backward(const evkhip_tensor* grad_out, const evkhip_tensor* indices,
+                          const evkhip_tensor* grad_embeddings, void* stream);
+
+/* ---------------------------------------------------------------------------
  * KV-cached greedy decode (the caller the single-query path exists for; the
  * reference decodes by full recompute, example/main_llm.cpp:622-654).  The
  * model is the reference block (main_llm.cpp:528-546) in multi-head,

@@ -97,6 +97,26 @@ def lib():
         L.orc_model_step.restype = C.c_uint32
         L.orc_model_step.argtypes = [C.POINTER(ModelCfg), u16p, u16p, C.c_uint16, C.c_uint32,
                                      u16p]
+        # training ops
+        L.orc_scale.argtypes = [u16p, C.c_float, C.c_uint64]
+        L.orc_relu.argtypes = [u16p, u16p, C.c_uint64]
+        L.orc_relu_bwd.argtypes = [u16p, u16p, u16p, C.c_uint64]
+        L.orc_gelu_grad_f32.restype = C.c_float
+        L.orc_gelu_grad_f32.argtypes = [C.c_float]
+        L.orc_gelu_bwd.argtypes = [u16p, u16p, u16p, C.c_uint64]
+        L.orc_sgd.argtypes = [u16p, u16p, C.c_float, C.c_uint64]
+        L.orc_adam.argtypes = [u16p, u16p, u16p, u16p, C.c_uint64] + [C.c_float] * 6
+        L.orc_softmax.argtypes = [u16p, u16p, C.c_float, C.c_uint64, C.c_uint32]
+        L.orc_softmax_bwd.argtypes = [u16p, u16p, u16p, C.c_float, C.c_uint64, C.c_uint32]
+        L.orc_rms_norm_bwd.argtypes = [u16p, u16p, u16p, C.c_float, C.c_uint64, C.c_uint32]
+        L.orc_mse_loss.argtypes = [u16p, u16p, u16p, u16p, C.c_uint64]
+        L.orc_cross_entropy.argtypes = [u16p, u16p, u16p, u16p, C.c_uint64, C.c_uint32]
+        L.orc_sum_batch.argtypes = [u16p, u16p, C.c_uint32, C.c_uint64]
+        L.orc_causal_mask.argtypes = [u16p, C.c_uint64, C.c_uint32]
+        L.orc_position_add.argtypes = [u16p, u16p, u16p, C.c_uint32, C.c_uint64]
+        L.orc_position_add_bwd.argtypes = [u16p, u16p, u16p, C.c_uint32, C.c_uint64]
+        L.orc_rope_bwd.argtypes = [u16p, u16p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float]
+        L.orc_embed_bwd.argtypes = [u16p, u16p, u16p, C.c_uint64, C.c_uint32, C.c_uint32]
         _LIB = L
     return _LIB
 
@@ -294,3 +314,132 @@ def model_step(cfg: ModelCfg, weights, cache, token, pos):
     logits = np.empty(cfg.vocab, np.uint16)
     nid = lib().orc_model_step(C.byref(cfg), _c(weights), cache, int(token), int(pos), logits)
     return nid, logits
+
+
+# ---------------------------------------------------------------------------
+# Training ops.  fp16 arrays are uint16 bit patterns; functions that update
+# in place in the reference (accumulated gradients, optimiser state) return
+# updated copies here.
+
+
+def scale(x, factor):
+    out = _c(x).copy()
+    lib().orc_scale(out.reshape(-1), factor, out.size)
+    return out
+
+
+def relu(x):
+    x = _c(x)
+    out = np.empty_like(x)
+    lib().orc_relu(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def relu_backward(grad_out, x, grad_in):
+    g, x, out = _c(grad_out), _c(x), _c(grad_in).copy()
+    lib().orc_relu_bwd(g.reshape(-1), x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def gelu_grad_f32(x):
+    return lib().orc_gelu_grad_f32(float(x))
+
+
+def gelu_backward(grad_out, x, grad_in):
+    g, x, out = _c(grad_out), _c(x), _c(grad_in).copy()
+    lib().orc_gelu_bwd(g.reshape(-1), x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def sgd(param, grad, lr):
+    out, g = _c(param).copy(), _c(grad)
+    lib().orc_sgd(out.reshape(-1), g.reshape(-1), lr, out.size)
+    return out
+
+
+def adam(param, grad, m, v, lr, beta1, beta2, c1inv, c2inv, eps):
+    """One step; returns (param, m, v) updated."""
+    p, g, m, v = _c(param).copy(), _c(grad), _c(m).copy(), _c(v).copy()
+    lib().orc_adam(p.reshape(-1), g.reshape(-1), m.reshape(-1), v.reshape(-1), p.size,
+                   lr, beta1, beta2, c1inv, c2inv, eps)
+    return p, m, v
+
+
+def softmax(x, scale=1.0):
+    x = _c(x)
+    out = np.empty_like(x)
+    D = x.shape[-1]
+    lib().orc_softmax(x.reshape(-1), out.reshape(-1), scale, x.size // D, D)
+    return out
+
+
+def softmax_backward(probs, grad_out, grad_in, scale=1.0):
+    p, g, out = _c(probs), _c(grad_out), _c(grad_in).copy()
+    D = p.shape[-1]
+    lib().orc_softmax_bwd(p.reshape(-1), g.reshape(-1), out.reshape(-1), scale, p.size // D, D)
+    return out
+
+
+def rms_norm_backward(x, grad_out, grad_in, eps=1e-4):
+    x, g, out = _c(x), _c(grad_out), _c(grad_in).copy()
+    D = x.shape[-1]
+    lib().orc_rms_norm_bwd(x.reshape(-1), g.reshape(-1), out.reshape(-1), eps, x.size // D, D)
+    return out
+
+
+def mse_loss(pred, target):
+    """Returns (grad, result[1])."""
+    p, t = _c(pred), _c(target)
+    grad = np.empty_like(p)
+    res = np.zeros(1, np.uint16)
+    lib().orc_mse_loss(p.reshape(-1), t.reshape(-1), grad.reshape(-1), res, p.size)
+    return grad, res
+
+
+def cross_entropy_loss(logits, targets):
+    """logits (P, V) fp16 bits, targets (P) uint16 ids; returns (grad, result[1])."""
+    x, t = _c(logits), _c(targets)
+    P, V = x.shape
+    grad = np.empty_like(x)
+    res = np.zeros(1, np.uint16)
+    lib().orc_cross_entropy(x.reshape(-1), t.reshape(-1), grad.reshape(-1), res, P, V)
+    return grad, res
+
+
+def sum_batch(x, out, batch, per):
+    x, o = _c(x), _c(out).copy()
+    lib().orc_sum_batch(x.reshape(-1), o.reshape(-1), batch, per)
+    return o
+
+
+def apply_causal_mask(scores):
+    out = _c(scores).copy()
+    N = out.shape[-1]
+    lib().orc_causal_mask(out.reshape(-1), out.size // (N * N), N)
+    return out
+
+
+def position_add(x, pos, batch, seq, dim):
+    x, pe = _c(x), _c(pos)
+    out = np.empty_like(x)
+    lib().orc_position_add(x.reshape(-1), pe.reshape(-1), out.reshape(-1), batch, seq * dim)
+    return out
+
+
+def position_add_backward(grad_out, grad_in, grad_pos, batch, seq, dim):
+    g, gi, gp = _c(grad_out), _c(grad_in).copy(), _c(grad_pos).copy()
+    lib().orc_position_add_bwd(g.reshape(-1), gi.reshape(-1), gp.reshape(-1), batch, seq * dim)
+    return gi, gp
+
+
+def rope_backward(grad_out, grad_in, batch, seq, dim, base=10000.0):
+    g, out = _c(grad_out), _c(grad_in).copy()
+    lib().orc_rope_bwd(g.reshape(-1), out.reshape(-1), batch, seq, dim, base)
+    return out
+
+
+def embed_backward(grad_out, idx, grad_emb):
+    g, i, out = _c(grad_out), _c(idx), _c(grad_emb).copy()
+    vocab, dim = out.shape
+    lib().orc_embed_bwd(g.reshape(-1), i.reshape(-1), out.reshape(-1), i.size, dim, vocab)
+    return out

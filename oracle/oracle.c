@@ -27,6 +27,11 @@
  *   greedy           : tests.h:1472-1497 KAT, brute-force total order.
  *   decode model     : composition of the above; small-model step-by-step
  *                      equality with a numpy restatement.
+ *   training ops     : reference KATs tests.h:221-399,619-730,1109-1470;
+ *                      fp64 Adam, finite differences (gelu', rms_norm
+ *                      backward), softmax Jacobian, rope adjoint identity,
+ *                      closed forms (mask, sum_batch, embed backward order)
+ *                      in tests/test_oracle_train.py.
  */
 #include <math.h>
 #include <stdint.h>
@@ -661,4 +666,252 @@ EXPORT void orc_model_generate(const orc_model_cfg* c, const uint16_t* w, uint16
 EXPORT uint32_t orc_model_step(const orc_model_cfg* c, const uint16_t* w, uint16_t* cache,
                                uint16_t token, uint32_t pos, uint16_t* logits) {
     return orc_model_forward(c, w, cache, &token, 1, pos, logits);
+}
+
+/* ======================================================================== */
+/* Training ops (the reference's non-inference shaders).  In-place outputs   */
+/* (gradients the shader accumulates into, optimiser state) are updated in   */
+/* the caller's arrays.                                                      */
+/* ======================================================================== */
+
+/* scale.comp:14-20 */
+EXPORT void orc_scale(uint16_t* x, float s, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) x[i] = f2h(h2f(x[i]) * s);
+}
+
+/* relu.comp:14-20 */
+EXPORT void orc_relu(const uint16_t* in, uint16_t* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) {
+        float v = h2f(in[i]);
+        out[i] = f2h(v > 0.0f ? v : 0.0f);
+    }
+}
+
+/* relu_bwd.comp:15-23 */
+EXPORT void orc_relu_bwd(const uint16_t* gout, const uint16_t* in, uint16_t* gin, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i)
+        gin[i] = f2h(h2f(gin[i]) + (h2f(in[i]) > 0.0f ? h2f(gout[i]) : 0.0f));
+}
+
+/* gelu_bwd.comp:16-27: derivative of the tanh GELU */
+EXPORT float orc_gelu_grad_f32(float x) {
+    const float a = 0.7978845608028654f, b = 0.044715f;
+    float x2 = x * x, x3 = x2 * x;
+    float t = tanhf(a * (x + b * x3));
+    float sech2 = 1.0f - t * t;
+    float du = a * (1.0f + 3.0f * b * x2);
+    return 0.5f * (1.0f + t) + 0.5f * x * sech2 * du;
+}
+
+/* gelu_bwd.comp:29-37 */
+EXPORT void orc_gelu_bwd(const uint16_t* gout, const uint16_t* in, uint16_t* gin, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i)
+        gin[i] = f2h(h2f(gin[i]) + h2f(gout[i]) * orc_gelu_grad_f32(h2f(in[i])));
+}
+
+/* sgd.comp:15-24 */
+EXPORT void orc_sgd(uint16_t* param, const uint16_t* grad, float lr, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) param[i] = f2h(h2f(param[i]) - lr * h2f(grad[i]));
+}
+
+/* adam.comp:32-84 with the host's bias corrections (evk_ai.cpp:541-545):
+ * state m = m / rms, v = log2(rms) + 41 (0 = rms 0), fp16 */
+EXPORT void orc_adam(uint16_t* param, const uint16_t* grad, uint16_t* m_s, uint16_t* v_s, uint64_t n,
+                     float lr, float b1, float b2, float c1inv, float c2inv, float eps) {
+    for (uint64_t i = 0; i < n; ++i) {
+        float g = h2f(grad[i]);
+        float stored = h2f(v_s[i]);
+        float rms = stored > 0.0f ? exp2f(stored - 41.0f) : 0.0f;
+        float m = h2f(m_s[i]) * rms, v = rms * rms;
+        if (isnan(g) || isinf(g)) continue;
+        m = b1 * m + (1.0f - b1) * g;
+        v = b2 * v + (1.0f - b2) * g * g;
+        rms = sqrtf(v > 0.0f ? v : 0.0f);
+        float mn = m / (rms > 1.0e-8f ? rms : 1.0e-8f);
+        if (!isnan(mn) && !isinf(mn)) m_s[i] = f2h(mn);
+        float lr2 = log2f(rms > 1.0e-12f ? rms : 1.0e-12f) + 41.0f;
+        if (!isnan(lr2) && !isinf(lr2)) v_s[i] = f2h(lr2);
+        float upd = lr * (m * c1inv) / (rms * sqrtf(c2inv) + eps);
+        if (!isnan(upd) && !isinf(upd)) {
+            float p = h2f(param[i]) - upd;
+            p = p < -65504.0f ? -65504.0f : (p > 65504.0f ? 65504.0f : p);
+            param[i] = f2h(p);
+        }
+    }
+}
+
+/* softmax.comp:21-69: per row of D, over in * scale; raw values <= -65504
+ * are masked (output 0); sums in double here */
+EXPORT void orc_softmax(const uint16_t* in, uint16_t* out, float scale, uint64_t rows, uint32_t D) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint16_t* x = in + r * D;
+        uint16_t* y = out + r * D;
+        float mx = -3.402823466e+38f;
+        for (uint32_t j = 0; j < D; ++j) {
+            float v = h2f(x[j]);
+            if (v > -65504.0f && v * scale > mx) mx = v * scale;
+        }
+        double sum = 0.0;
+        for (uint32_t j = 0; j < D; ++j) {
+            float v = h2f(x[j]);
+            if (v > -65504.0f) sum += exp((double)(v * scale - mx));
+        }
+        double inv = 1.0 / (sum > 1e-20 ? sum : 1e-20);
+        for (uint32_t j = 0; j < D; ++j) {
+            float v = h2f(x[j]);
+            y[j] = f2h(v > -65504.0f ? (float)(exp((double)(v * scale - mx)) * inv) : 0.0f);
+        }
+    }
+}
+
+/* softmax_bwd.comp:20-43: grad_in += p (g - p.g) scale per row */
+EXPORT void orc_softmax_bwd(const uint16_t* probs, const uint16_t* gout, uint16_t* gin, float scale,
+                            uint64_t rows, uint32_t D) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint16_t* p = probs + r * D;
+        const uint16_t* g = gout + r * D;
+        uint16_t* o = gin + r * D;
+        double dot = 0.0;
+        for (uint32_t j = 0; j < D; ++j) dot += (double)h2f(p[j]) * h2f(g[j]);
+        for (uint32_t j = 0; j < D; ++j)
+            o[j] = f2h(h2f(o[j]) + (float)((double)h2f(p[j]) * (h2f(g[j]) - dot) * scale));
+    }
+}
+
+/* rms_norm_bwd.comp:24-70: grad_in += g/rms - x (g.y) / (D rms^2), y = x/rms,
+ * rms = sqrt(mean(x^2) + eps), x clamped to the fp16 range */
+EXPORT void orc_rms_norm_bwd(const uint16_t* in, const uint16_t* gout, uint16_t* gin, float eps,
+                             uint64_t rows, uint32_t D) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint16_t* x = in + r * D;
+        const uint16_t* g = gout + r * D;
+        uint16_t* o = gin + r * D;
+        double ss = 0.0;
+        for (uint32_t j = 0; j < D; ++j) {
+            double v = fmin(fmax(h2f(x[j]), -65504.0), 65504.0);
+            ss += v * v;
+        }
+        double inv = 1.0 / sqrt(ss / D + eps);
+        double dot = 0.0;
+        for (uint32_t j = 0; j < D; ++j) dot += h2f(g[j]) * (fmin(fmax(h2f(x[j]), -65504.0), 65504.0) * inv);
+        double sc = dot / D;
+        for (uint32_t j = 0; j < D; ++j) {
+            double v = fmin(fmax(h2f(x[j]), -65504.0), 65504.0);
+            o[j] = f2h((float)(h2f(o[j]) + (h2f(g[j]) * inv - v * inv * inv * sc)));
+        }
+    }
+}
+
+/* mse_loss.comp:23-48: grad = 2 (p - t) / n, result = sum (p - t)^2 / n */
+EXPORT void orc_mse_loss(const uint16_t* pred, const uint16_t* tgt, uint16_t* grad, uint16_t* result, uint64_t n) {
+    double s = 0.0;
+    const float gs = 2.0f / (float)n;
+    for (uint64_t i = 0; i < n; ++i) {
+        float d = h2f(pred[i]) - h2f(tgt[i]);
+        s += (double)d * d;
+        grad[i] = f2h(gs * d);
+    }
+    result[0] = f2h((float)(s / (double)n));
+}
+
+/* cross_entropy_count.comp, cross_entropy.comp:27-106, cross_entropy_scale.comp:
+ * targets 0 or >= V are ignored (zero gradient row); logits clamped to
+ * +-65000; grad = (softmax - onehot) / n_valid; result = mean loss over the
+ * valid rows (0 if none or not finite) */
+EXPORT void orc_cross_entropy(const uint16_t* logits, const uint16_t* targets, uint16_t* grad, uint16_t* result,
+                              uint64_t P, uint32_t V) {
+    uint64_t valid = 0;
+    for (uint64_t r = 0; r < P; ++r)
+        if (targets[r] != 0 && targets[r] < V) ++valid;
+    double total = 0.0;
+    for (uint64_t r = 0; r < P; ++r) {
+        const uint16_t* x = logits + r * V;
+        uint16_t* g = grad + r * V;
+        uint32_t t = targets[r];
+        if (t == 0 || t >= V || valid == 0) {
+            for (uint32_t j = 0; j < V; ++j) g[j] = 0;
+            continue;
+        }
+        double inv_valid = 1.0 / (double)valid;
+        double mx = -3.402823466e+38;
+        for (uint32_t j = 0; j < V; ++j) {
+            double v = fmin(fmax(h2f(x[j]), -65000.0), 65000.0);
+            if (v > mx) mx = v;
+        }
+        double sum = 0.0;
+        for (uint32_t j = 0; j < V; ++j) sum += exp(fmin(fmax(h2f(x[j]), -65000.0), 65000.0) - mx);
+        if (sum < 1e-20) sum = 1e-20;
+        for (uint32_t j = 0; j < V; ++j) {
+            double v = fmin(fmax(h2f(x[j]), -65000.0), 65000.0);
+            double gv = exp(v - mx) / sum * inv_valid;
+            if (j == t) gv -= inv_valid;
+            g[j] = f2h((float)gv);
+        }
+        double vt = fmin(fmax(h2f(x[t]), -65000.0), 65000.0);
+        total += (mx + log(sum) - vt) * inv_valid;
+    }
+    float loss = valid > 0 ? (float)total : 0.0f;
+    if (isnan(loss) || isinf(loss)) loss = 0.0f;
+    result[0] = f2h(loss);
+}
+
+/* sum_batch.comp:14-24: out[i] = out[i] + sum_b in[b, i], one rounding */
+EXPORT void orc_sum_batch(const uint16_t* in, uint16_t* out, uint32_t batch, uint64_t per) {
+    for (uint64_t i = 0; i < per; ++i) {
+        float s = h2f(out[i]);
+        for (uint32_t b = 0; b < batch; ++b) s += h2f(in[(uint64_t)b * per + i]);
+        out[i] = f2h(s);
+    }
+}
+
+/* causal_mask.comp:13-30: scores[b, i, j] = -65504 for j > i */
+EXPORT void orc_causal_mask(uint16_t* scores, uint64_t batch, uint32_t N) {
+    const uint16_t neg = orc_f32_to_f16(-65504.0f);
+    for (uint64_t b = 0; b < batch; ++b)
+        for (uint32_t i = 0; i < N; ++i)
+            for (uint32_t j = i + 1; j < N; ++j) scores[(b * N + i) * N + j] = neg;
+}
+
+/* position_add.comp:17-34 */
+EXPORT void orc_position_add(const uint16_t* in, const uint16_t* pos, uint16_t* out, uint32_t B, uint64_t per) {
+    for (uint32_t b = 0; b < B; ++b)
+        for (uint64_t i = 0; i < per; ++i) out[b * per + i] = f2h(h2f(in[b * per + i]) + h2f(pos[i]));
+}
+
+/* position_add_bwd.comp:20-49, both modes */
+EXPORT void orc_position_add_bwd(const uint16_t* gout, uint16_t* gin, uint16_t* gpos, uint32_t B, uint64_t per) {
+    for (uint64_t i = 0; i < (uint64_t)B * per; ++i) gin[i] = f2h(h2f(gin[i]) + h2f(gout[i]));
+    for (uint64_t i = 0; i < per; ++i) {
+        float s = h2f(gpos[i]);
+        for (uint32_t b = 0; b < B; ++b) s += h2f(gout[b * per + i]);
+        gpos[i] = f2h(s);
+    }
+}
+
+/* rope_bwd.comp:15-45: grad_in += R(t)^T grad_out per pair */
+EXPORT void orc_rope_bwd(const uint16_t* gout, uint16_t* gin, uint32_t B, uint32_t S, uint32_t E, float base) {
+    for (uint32_t b = 0; b < B; ++b)
+        for (uint32_t t = 0; t < S; ++t)
+            for (uint32_t p = 0; p < E / 2; ++p) {
+                uint64_t i = ((uint64_t)b * S + t) * E + 2 * p;
+                float g0 = h2f(gout[i]), g1 = h2f(gout[i + 1]);
+                float inv_freq = powf(base, -2.0f * (float)p / (float)E);
+                float c = cosf((float)t * inv_freq), s = sinf((float)t * inv_freq);
+                gin[i] = f2h(h2f(gin[i]) + (g0 * c + g1 * s));
+                gin[i + 1] = f2h(h2f(gin[i + 1]) + (-g0 * s + g1 * c));
+            }
+}
+
+/* embed_bwd.comp:16-32: grad_emb[idx[r]] += grad_out[r] for r in order, one
+ * fp16 rounding per addition; ids >= vocab skipped */
+EXPORT void orc_embed_bwd(const uint16_t* gout, const uint16_t* idx, uint16_t* gemb, uint64_t n_idx, uint32_t dim,
+                          uint32_t vocab) {
+    for (uint64_t r = 0; r < n_idx; ++r) {
+        uint32_t tok = idx[r];
+        if (tok >= vocab) continue;
+        for (uint32_t d = 0; d < dim; ++d) {
+            uint16_t* dst = gemb + (uint64_t)tok * dim + d;
+            *dst = f2h(h2f(*dst) + h2f(gout[r * dim + d]));
+        }
+    }
 }
