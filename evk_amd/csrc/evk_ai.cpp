@@ -5,7 +5,9 @@
 // (:13-28), initialize/shutdown (:211-252), matmul (:254-330),
 // flash_attention (:332-369), flash_attention_bwd (:371-473), add
 // (:568-591), gelu (:679-699), embed (:782-806), greedy_sample (:808-837),
-// rope (:945-966), zero (:1010-1025), rms_norm (:1045-1067).  Shape checks
+// rope (:945-966), zero (:1010-1025), rms_norm (:1045-1067), and the
+// training ops with AdamState (:181-209,475-566,593-780,839-943,968-1043,
+// 1072-1093).  Shape checks
 // live in the C ABI (they run on the host before any launch); a failed check
 // prints the library's message and aborts, as the reference's asserts do.
 #include <evk_ai.h>
@@ -148,6 +150,125 @@ void zero(Tensor& tensor) {
         std::fprintf(stderr, "evk::ai::zero failed: %s\n", hipGetErrorString(e));
         std::abort();
     }
+}
+
+// ---- training ops (evk_ai.cpp:475-566,593-780,839-943,968-1043,1072-1093) ----
+
+void AdamState::init(uint32_t num_elements) {
+    const uint64_t bytes = uint64_t(num_elements) * sizeof(float16_t);
+    m_buffer = evk::CreateBuffer({.size = bytes, .usage = evk::BufferUsage::Storage | evk::BufferUsage::TransferDst});
+    v_buffer = evk::CreateBuffer({.size = bytes, .usage = evk::BufferUsage::Storage | evk::BufferUsage::TransferDst});
+    if (bytes) {
+        GetCmd().fill(m_buffer, 0u, bytes);
+        GetCmd().fill(v_buffer, 0u, bytes);
+    }
+    t = 0;
+}
+
+void AdamState::reset() {
+    m_buffer = {};
+    v_buffer = {};
+    t = 0;
+}
+
+void mse_loss(Tensor& predicted, Tensor& target, Tensor& predGrad, Tensor& result) {
+    evkhip_tensor P = desc(predicted), T = desc(target), G = desc(predGrad), R = desc(result);
+    check(evkhip_mse_loss(&P, &T, &G, &R, stream()), "mse_loss");
+}
+
+void sgd(Tensor& param, Tensor& gradient, float learning_rate) {
+    evkhip_tensor P = desc(param), G = desc(gradient);
+    check(evkhip_sgd(&P, &G, learning_rate, stream()), "sgd");
+}
+
+void adam(Tensor& param, Tensor& gradient, AdamState& state, float learning_rate, float beta1, float beta2,
+          float epsilon) {
+    const uint32_t n = param.shape.count();
+    if (!state.m_buffer) state.init(n);
+    state.t++;
+    const float c1 = 1.0f / (1.0f - std::pow(beta1, float(state.t)));
+    const float c2 = 1.0f / (1.0f - std::pow(beta2, float(state.t)));
+    evkhip_tensor P = desc(param), G = desc(gradient);
+    evkhip_tensor M{}, V{};
+    M.data = reinterpret_cast<void*>(state.m_buffer.GetReference());
+    V.data = reinterpret_cast<void*>(state.v_buffer.GetReference());
+    M.rank = V.rank = 1;
+    M.dims[0] = V.dims[0] = n;
+    check(evkhip_adam(&P, &G, &M, &V, learning_rate, beta1, beta2, c1, c2, epsilon, stream()), "adam");
+}
+
+void softmax(Tensor& in, Tensor& out, float input_scale) {
+    evkhip_tensor I = desc(in), O = desc(out);
+    check(evkhip_softmax(&I, &O, input_scale, stream()), "softmax");
+}
+
+void softmax_backward(Tensor& probs, Tensor& grad_out, Tensor& grad_in, float scale_factor) {
+    evkhip_tensor P = desc(probs), G = desc(grad_out), I = desc(grad_in);
+    check(evkhip_softmax_backward(&P, &G, &I, scale_factor, stream()), "softmax_backward");
+}
+
+void relu(Tensor& in, Tensor& out) {
+    evkhip_tensor I = desc(in), O = desc(out);
+    check(evkhip_relu(&I, &O, stream()), "relu");
+}
+
+void relu_backward(Tensor& grad_out, Tensor& in, Tensor& grad_in) {
+    evkhip_tensor G = desc(grad_out), I = desc(in), D = desc(grad_in);
+    check(evkhip_relu_backward(&G, &I, &D, stream()), "relu_backward");
+}
+
+void gelu_backward(Tensor& grad_out, Tensor& in, Tensor& grad_in) {
+    evkhip_tensor G = desc(grad_out), I = desc(in), D = desc(grad_in);
+    check(evkhip_gelu_backward(&G, &I, &D, stream()), "gelu_backward");
+}
+
+void cross_entropy_loss(Tensor& logits, Tensor& targets, Tensor& grad, Tensor& result) {
+    evkhip_tensor L = desc(logits), T = desc(targets), G = desc(grad), R = desc(result);
+    check(evkhip_cross_entropy_loss(&L, &T, &G, &R, stream()), "cross_entropy_loss");
+}
+
+void embed_backward(Tensor& grad_out, Tensor& indices, Tensor& grad_embeddings) {
+    evkhip_tensor G = desc(grad_out), I = desc(indices), E = desc(grad_embeddings);
+    check(evkhip_embed_backward(&G, &I, &E, stream()), "embed_backward");
+}
+
+void apply_causal_mask(Tensor& scores) {
+    evkhip_tensor S = desc(scores);
+    check(evkhip_apply_causal_mask(&S, stream()), "apply_causal_mask");
+}
+
+void position_add(Tensor& input, Tensor& pos_emb, Tensor& out, uint32_t batch_size, uint32_t seq_len,
+                  uint32_t embed_dim) {
+    evkhip_tensor I = desc(input), P = desc(pos_emb), O = desc(out);
+    check(evkhip_position_add(&I, &P, &O, batch_size, seq_len, embed_dim, stream()), "position_add");
+}
+
+void position_add_backward(Tensor& grad_out, Tensor& grad_input, Tensor& grad_pos, uint32_t batch_size,
+                           uint32_t seq_len, uint32_t embed_dim) {
+    evkhip_tensor G = desc(grad_out), I = desc(grad_input), P = desc(grad_pos);
+    check(evkhip_position_add_backward(&G, &I, &P, batch_size, seq_len, embed_dim, stream()),
+          "position_add_backward");
+}
+
+void rope_backward(Tensor& grad_out, Tensor& grad_input, uint32_t batch_size, uint32_t seq_len, uint32_t embed_dim,
+                   float rotary_base) {
+    evkhip_tensor G = desc(grad_out), I = desc(grad_input);
+    check(evkhip_rope_backward(&G, &I, batch_size, seq_len, embed_dim, rotary_base, stream()), "rope_backward");
+}
+
+void scale(Tensor& tensor, float scale_factor) {
+    evkhip_tensor T = desc(tensor);
+    check(evkhip_scale(&T, scale_factor, stream()), "scale");
+}
+
+void sum_batch(Tensor& input, Tensor& output, uint32_t batch_count, uint32_t size_per_batch) {
+    evkhip_tensor I = desc(input), O = desc(output);
+    check(evkhip_sum_batch(&I, &O, batch_count, size_per_batch, stream()), "sum_batch");
+}
+
+void rms_norm_backward(Tensor& input, Tensor& grad_out, Tensor& grad_input, float eps) {
+    evkhip_tensor I = desc(input), G = desc(grad_out), D = desc(grad_input);
+    check(evkhip_rms_norm_backward(&I, &G, &D, eps, stream()), "rms_norm_backward");
 }
 
 }  // namespace evk::ai

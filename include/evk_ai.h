@@ -27,6 +27,7 @@
 #include <functional>
 #include <initializer_list>
 #include <memory>
+#include <unordered_map>
 #include <vector>
 
 namespace evk::ai {
@@ -385,4 +386,360 @@ void rms_norm(Tensor& input, Tensor& output, float eps = 1e-4f);
 // tensor = 0 (evk_ai.h:602).
 void zero(Tensor& tensor);
 
+// ---- training ops (evk_ai.h:476-614).  *_backward ops accumulate into
+// their grad_in, as the reference's shaders do. ----
+
+// Adam state of one parameter tensor (evk_ai.h:476-487): fp16 first moment
+// divided by the RMS of the second moment, and log2 of that RMS plus 41
+// (0 meaning RMS 0); t counts the steps taken.
+struct AdamState {
+    evk::Buffer m_buffer;
+    evk::Buffer v_buffer;
+    uint32_t t = 0;
+
+    void init(uint32_t num_elements);  // zeroed state, t = 0
+    void reset();                      // releases the state
+};
+
+// result[0] = mean((predicted - target)^2); predGrad = 2 (predicted - target) / n
+// (evk_ai.h:505-507).
+void mse_loss(Tensor& predicted, Tensor& target, Tensor& predGrad, Tensor& result);
+
+// param -= learning_rate * gradient (evk_ai.h:509-510).
+void sgd(Tensor& param, Tensor& gradient, float learning_rate);
+
+// One Adam step; the state is created on first use and t advances by one
+// (evk_ai.h:512-518).
+void adam(Tensor& param, Tensor& gradient, AdamState& state, float learning_rate = 0.001f, float beta1 = 0.9f,
+          float beta2 = 0.999f, float epsilon = 1e-4f);
+
+// Softmax over the last dimension of in * input_scale; entries <= -65504 are
+// masked to probability 0 (evk_ai.h:523-525).
+void softmax(Tensor& in, Tensor& out, float input_scale = 1.0f);
+
+// grad_in += probs * (grad_out - dot(grad_out, probs)) * scale_factor per row
+// (evk_ai.h:527-529).
+void softmax_backward(Tensor& probs, Tensor& grad_out, Tensor& grad_in, float scale_factor = 1.0f);
+
+// out = max(0, in); grad_in += (in > 0 ? grad_out : 0) (evk_ai.h:531-536).
+void relu(Tensor& in, Tensor& out);
+void relu_backward(Tensor& grad_out, Tensor& in, Tensor& grad_in);
+
+// grad_in += grad_out * gelu'(in) (evk_ai.h:542-543).
+void gelu_backward(Tensor& grad_out, Tensor& in, Tensor& grad_in);
+
+// logits (B*N, V), targets (B*N) raw uint16 (0 = ignore): grad = (softmax -
+// one_hot) / n_valid, zero rows for ignored targets; result[0] = mean loss
+// over the valid rows (evk_ai.h:545-552).
+void cross_entropy_loss(Tensor& logits, Tensor& targets, Tensor& grad, Tensor& result);
+
+// grad_embeddings[indices[i]] += grad_out[i] (evk_ai.h:568-572).
+void embed_backward(Tensor& grad_out, Tensor& indices, Tensor& grad_embeddings);
+
+// scores (..., N, N): entries j > i set to -65504 (evk_ai.h:574-577).
+void apply_causal_mask(Tensor& scores);
+
+// out = input + pos_emb broadcast over the batch; backward: grad_input +=
+// grad_out, grad_pos += sum over the batch (evk_ai.h:579-585).
+void position_add(Tensor& input, Tensor& pos_emb, Tensor& out, uint32_t batch_size, uint32_t seq_len,
+                  uint32_t embed_dim);
+void position_add_backward(Tensor& grad_out, Tensor& grad_input, Tensor& grad_pos, uint32_t batch_size,
+                           uint32_t seq_len, uint32_t embed_dim);
+
+// grad_input += the transposed rotation of grad_out (evk_ai.h:593-596).
+void rope_backward(Tensor& grad_out, Tensor& grad_input, uint32_t batch_size, uint32_t seq_len,
+                   uint32_t embed_dim, float rotary_base = 10000.0f);
+
+// tensor *= scale_factor in place (evk_ai.h:598-599).
+void scale(Tensor& tensor, float scale_factor);
+
+// output[i] += sum_b input[b * size_per_batch + i] (evk_ai.h:604-605).
+void sum_batch(Tensor& input, Tensor& output, uint32_t batch_count, uint32_t size_per_batch);
+
+// grad_input += (g - y dot(g, y) / D) / rms per row (evk_ai.h:612-614).
+void rms_norm_backward(Tensor& input, Tensor& grad_out, Tensor& grad_input, float eps = 1e-4f);
+
 }  // namespace evk::ai
+
+// A define-by-run graph with reverse-mode gradients (evk_ai.h:616-1074).
+// Ops append nodes whose forward_fn / backward_fn record work on the
+// library stream; eval() runs them in order (and the backward functions in
+// reverse), step()/step_adam() update the parameters.  Gradient buffers
+// accumulate, and eval(true) zeroes them first, as in the reference.
+// causal_attention runs the fused causal flash attention (forward with the
+// saved log-sum-exp, backward from it) instead of materialising the N x N
+// scores and probabilities; a non-default scale takes the unfused
+// matmul / mask / softmax / matmul chain.
+struct Graph {
+    std::vector<std::unique_ptr<Tensor>> nodes;
+    std::vector<Tensor*> params;
+    std::unordered_map<Tensor*, evk::ai::AdamState> adam_states;
+    std::unique_ptr<Tensor> scratch;
+
+    Tensor& get_scratch(const Shape& shape) {
+        if (!scratch || scratch->shape.count() < shape.count()) {
+            scratch = std::make_unique<Tensor>(shape);
+        } else {
+            scratch->shape = shape;
+        }
+        return *scratch;
+    }
+
+    Tensor& tensor(Shape shape, bool param = false) {
+        Tensor& t = node(shape);
+        if (param) params.push_back(&t);
+        return t;
+    }
+
+    // Same elements under another shape (a copy of the buffer each eval).
+    Tensor& view(Tensor& a, Shape new_shape) {
+        assert(a.shape.count() == new_shape.count() && "view requires the same number of elements");
+        Tensor& out = node(new_shape);
+        const uint64_t bytes = uint64_t(a.shape.count()) * sizeof(float16_t);
+        out.forward_fn = [&a, &out, bytes]() { evk::ai::GetCmd().copy(a.buffer, out.buffer, bytes); };
+        out.backward_fn = [&a, &out, bytes]() { evk::ai::GetCmd().copy(out.grad().buffer, a.grad().buffer, bytes); };
+        return out;
+    }
+
+    // (M,K)@(K,N), (B,M,K)@(K,N), (M,K)@(B,K,N) and (B,M,K)@(B,K,N).
+    Tensor& matmul(Tensor& a, Tensor& b, uint8_t tile_m = 16, uint8_t tile_n = 16) {
+        const uint32_t ra = a.shape.rank(), rb = b.shape.rank();
+        Shape out_shape;
+        if (ra == 2 && rb == 2) {
+            out_shape = Shape({a.shape[0], b.shape[1]});
+        } else if (ra == 3 && rb == 2) {
+            out_shape = Shape({a.shape[0], a.shape[1], b.shape[1]});
+        } else if (ra == 2 && rb == 3) {
+            out_shape = Shape({b.shape[0], a.shape[0], b.shape[2]});
+        } else if (ra == 3 && rb == 3) {
+            out_shape = Shape({a.shape[0], a.shape[1], b.shape[2]});
+        } else {
+            assert(false && "Graph::matmul: unsupported ranks");
+        }
+        Tensor& c = node(out_shape);
+        c.forward_fn = [&a, &b, &c, tile_m, tile_n]() {
+            evk::ai::matmul(a, b, c, false, false, false, tile_m, tile_n);
+        };
+        c.backward_fn = [this, &a, &b, &c, tile_m, tile_n]() {
+            // dA += dC B^T
+            evk::ai::matmul(c.grad(), b, a.grad(), false, true, true, tile_m, tile_n);
+            // dB += A^T dC; a batched A against a shared B sums the batch
+            if (a.shape.rank() == 3 && b.shape.rank() == 2) {
+                const uint32_t B = a.shape[0], K = a.shape[2], N = b.shape[1];
+                Tensor& per_batch = get_scratch(Shape({B, K, N}));
+                evk::ai::matmul(a, c.grad(), per_batch, true, false, false, tile_m, tile_n);
+                evk::ai::sum_batch(per_batch, b.grad(), B, K * N);
+            } else {
+                evk::ai::matmul(a, c.grad(), b.grad(), true, false, true, tile_m, tile_n);
+            }
+        };
+        return c;
+    }
+
+    Tensor& add(Tensor& a, Tensor& b) {
+        Tensor& c = node(a.shape);
+        c.forward_fn = [&a, &b, &c]() { evk::ai::add(a, b, c); };
+        c.backward_fn = [&a, &b, &c]() {
+            evk::ai::add(a.grad(), c.grad(), a.grad());
+            evk::ai::add(b.grad(), c.grad(), b.grad());
+        };
+        return c;
+    }
+
+    // Scalar loss; the forward pass also writes predicted's gradient.
+    Tensor& mse_loss(Tensor& predicted, Tensor& target) {
+        assert(predicted.shape.rank() == target.shape.rank() && "mse_loss: ranks differ");
+        Tensor& loss = node(Shape({1}));
+        loss.forward_fn = [&predicted, &target, &loss]() {
+            evk::ai::mse_loss(predicted, target, predicted.grad(), loss);
+        };
+        return loss;
+    }
+
+    Tensor& relu(Tensor& a) {
+        Tensor& out = node(a.shape);
+        out.forward_fn = [&a, &out]() { evk::ai::relu(a, out); };
+        out.backward_fn = [&a, &out]() { evk::ai::relu_backward(out.grad(), a, a.grad()); };
+        return out;
+    }
+
+    Tensor& gelu(Tensor& a) {
+        Tensor& out = node(a.shape);
+        out.forward_fn = [&a, &out]() { evk::ai::gelu(a, out); };
+        out.backward_fn = [&a, &out]() { evk::ai::gelu_backward(out.grad(), a, a.grad()); };
+        return out;
+    }
+
+    Tensor& scale(Tensor& a, float factor) {
+        Tensor& out = node(a.shape);
+        const uint64_t bytes = uint64_t(a.shape.count()) * sizeof(float16_t);
+        out.forward_fn = [&a, &out, factor, bytes]() {
+            evk::ai::GetCmd().copy(a.buffer, out.buffer, bytes);
+            evk::ai::scale(out, factor);
+        };
+        out.backward_fn = [&a, &out, factor]() {
+            // out's consumers have all run their backward functions by now
+            evk::ai::scale(out.grad(), factor);
+            evk::ai::add(a.grad(), out.grad(), a.grad());
+        };
+        return out;
+    }
+
+    Tensor& rms_norm(Tensor& input, float eps = 1e-4f) {
+        assert(input.shape.rank() >= 2 && "rms_norm expects at least 2D tensor");
+        Tensor& out = node(input.shape);
+        out.forward_fn = [&input, &out, eps]() { evk::ai::rms_norm(input, out, eps); };
+        out.backward_fn = [&input, &out, eps]() { evk::ai::rms_norm_backward(input, out.grad(), input.grad(), eps); };
+        return out;
+    }
+
+    // input (B, N, D) + pos_emb (N, D) broadcast over the batch.
+    Tensor& add_position_embedding(Tensor& input, Tensor& pos_emb, uint32_t batch_size, uint32_t seq_len) {
+        const uint32_t dim = pos_emb.shape[1];
+        assert(input.shape.rank() == 3 && input.shape[0] == batch_size && input.shape[1] == seq_len &&
+               input.shape[2] == dim && pos_emb.shape[0] == seq_len && "add_position_embedding: shapes");
+        Tensor& out = node(input.shape);
+        out.forward_fn = [&input, &pos_emb, &out, batch_size, seq_len, dim]() {
+            evk::ai::position_add(input, pos_emb, out, batch_size, seq_len, dim);
+        };
+        out.backward_fn = [&input, &pos_emb, &out, batch_size, seq_len, dim]() {
+            evk::ai::position_add_backward(out.grad(), input.grad(), pos_emb.grad(), batch_size, seq_len, dim);
+        };
+        return out;
+    }
+
+    Tensor& rope(Tensor& input, float rotary_base = 10000.0f) {
+        assert(input.shape.rank() == 3 && input.shape[2] % 2 == 0 && "rope expects (B, N, D), D even");
+        const uint32_t B = input.shape[0], N = input.shape[1], D = input.shape[2];
+        Tensor& out = node(input.shape);
+        out.forward_fn = [&input, &out, B, N, D, rotary_base]() { evk::ai::rope(input, out, B, N, D, rotary_base); };
+        out.backward_fn = [&input, &out, B, N, D, rotary_base]() {
+            evk::ai::rope_backward(out.grad(), input.grad(), B, N, D, rotary_base);
+        };
+        return out;
+    }
+
+    // embeddings (V, D), indices (B, N) raw uint16 -> (B, N, D).
+    Tensor& embed(Tensor& embeddings, Tensor& indices) {
+        assert(indices.shape.rank() == 2 && "indices must be (B, N)");
+        Tensor& out = node(Shape({indices.shape[0], indices.shape[1], embeddings.shape[1]}));
+        out.forward_fn = [&embeddings, &indices, &out]() { evk::ai::embed(embeddings, indices, out); };
+        out.backward_fn = [&embeddings, &indices, &out]() {
+            evk::ai::embed_backward(out.grad(), indices, embeddings.grad());
+        };
+        return out;
+    }
+
+    // logits (B, N, V), targets (B, N) raw uint16, target 0 ignored -> scalar
+    // mean loss over the other positions.
+    Tensor& cross_entropy_loss(Tensor& logits, Tensor& targets) {
+        assert(logits.shape.rank() == 3 && targets.shape.rank() == 2 && "cross_entropy_loss: shapes");
+        const uint32_t rows = logits.shape[0] * logits.shape[1], V = logits.shape[2];
+        Tensor& flat_grad = node(Shape({rows, V}));
+        Tensor& loss = node(Shape({1}));
+        auto run = [&logits, &targets, &flat_grad, &loss, rows, V]() {
+            Tensor flat_logits = Tensor::alias(Shape({rows, V}), logits.buffer);
+            Tensor flat_targets = Tensor::alias(Shape({rows}), targets.buffer);
+            evk::ai::cross_entropy_loss(flat_logits, flat_targets, flat_grad, loss);
+        };
+        loss.forward_fn = run;
+        loss.backward_fn = [run, &logits, &flat_grad]() {
+            run();
+            evk::ai::GetCmd().copy(flat_grad.buffer, logits.grad().buffer,
+                                   uint64_t(logits.shape.count()) * sizeof(float16_t));
+        };
+        return loss;
+    }
+
+    Tensor& softmax(Tensor& input, float input_scale = 1.0f) {
+        Tensor& out = node(input.shape);
+        out.forward_fn = [&input, &out, input_scale]() { evk::ai::softmax(input, out, input_scale); };
+        out.backward_fn = [&input, &out, input_scale]() {
+            evk::ai::softmax_backward(out, out.grad(), input.grad(), input_scale);
+        };
+        return out;
+    }
+
+    // Causal self-attention of q, k, v (B, N, D): softmax(q k^T * scale with
+    // keys j > i masked) v; scale 0 means 1/sqrt(D).
+    Tensor& causal_attention(Tensor& q, Tensor& k, Tensor& v, float scale = 0.0f) {
+        assert(q.shape.rank() == 3 && k.shape.rank() == 3 && v.shape.rank() == 3 && "causal_attention: (B, N, D)");
+        const uint32_t B = q.shape[0], N = q.shape[1], D = q.shape[2];
+        const float default_scale = 1.0f / std::sqrt(float(D));
+        if (scale > 0.0f && scale != default_scale) return causal_attention_unfused(q, k, v, scale);
+        Tensor& lse = node(Shape({B, 1, N, 2}));  // fp32 log-sum-exp per row
+        Tensor& dq = node(q.shape);
+        Tensor& dk = node(k.shape);
+        Tensor& dv = node(v.shape);
+        Tensor& out = node(Shape({B, N, D}));
+        out.forward_fn = [&q, &k, &v, &out, &lse]() { evk::ai::flash_attention(q, k, v, out, true, &lse); };
+        out.backward_fn = [&q, &k, &v, &out, &lse, &dq, &dk, &dv]() {
+            evk::ai::flash_attention_bwd(q, k, v, out, out.grad(), dq, dk, dv, 1, true, &lse);
+            evk::ai::add(q.grad(), dq, q.grad());
+            evk::ai::add(k.grad(), dk, k.grad());
+            evk::ai::add(v.grad(), dv, v.grad());
+        };
+        return out;
+    }
+
+    // The reference's composition: scores = q k^T, mask, softmax(scale), @ v.
+    Tensor& causal_attention_unfused(Tensor& q, Tensor& k, Tensor& v, float scale = 0.0f) {
+        const uint32_t B = q.shape[0], N = q.shape[1], D = q.shape[2];
+        const float s = scale > 0.0f ? scale : 1.0f / std::sqrt(float(D));
+        Tensor& scores = node(Shape({B, N, N}));
+        Tensor& probs = node(Shape({B, N, N}));
+        Tensor& out = node(Shape({B, N, D}));
+        out.forward_fn = [&q, &k, &v, &scores, &probs, &out, s]() {
+            evk::ai::matmul(q, k, scores, false, true, false, 16, 16);
+            evk::ai::apply_causal_mask(scores);
+            evk::ai::softmax(scores, probs, s);
+            evk::ai::matmul(probs, v, out, false, false, false, 16, 16);
+        };
+        out.backward_fn = [&q, &k, &v, &scores, &probs, &out, s]() {
+            evk::ai::matmul(out.grad(), v, probs.grad(), false, true, false, 16, 16);
+            evk::ai::matmul(probs, out.grad(), v.grad(), true, false, true, 16, 16);
+            evk::ai::softmax_backward(probs, probs.grad(), scores.grad(), s);
+            evk::ai::matmul(scores.grad(), k, q.grad(), false, false, true, 16, 16);
+            evk::ai::matmul(scores.grad(), q, k.grad(), true, false, true, 16, 16);
+        };
+        return out;
+    }
+
+    Tensor& residual(Tensor& a, Tensor& b) { return add(a, b); }
+
+    // Forward functions in order; with backward, gradients are zeroed first
+    // and the backward functions run in reverse order.
+    void eval(bool backward = false, bool submit = true, bool wait = true) {
+        evk::ai::GetCmd();
+        if (backward)
+            for (auto& n : nodes) evk::ai::zero(n->grad());
+        for (auto& n : nodes)
+            if (n->forward_fn) n->forward_fn();
+        if (backward)
+            for (auto it = nodes.rbegin(); it != nodes.rend(); ++it)
+                if ((*it)->backward_fn) (*it)->backward_fn();
+        if (submit) evk::ai::SubmitCmd(wait);
+    }
+
+    void step(float lr = 0.001f) {
+        for (Tensor* p : params) {
+            assert(p->grad_tensor && "Graph::step: parameter without a gradient");
+            evk::ai::sgd(*p, p->grad(), lr);
+        }
+    }
+
+    void step_adam(float lr = 0.001f, float beta1 = 0.9f, float beta2 = 0.999f, float epsilon = 1e-4f) {
+        for (Tensor* p : params) evk::ai::adam(*p, p->grad(), adam_states[p], lr, beta1, beta2, epsilon);
+    }
+
+    void reset_adam() {
+        for (auto& kv : adam_states) kv.second.reset();
+        adam_states.clear();
+    }
+
+private:
+    Tensor& node(const Shape& shape) {
+        nodes.push_back(std::make_unique<Tensor>(shape));
+        return *nodes.back();
+    }
+};

@@ -573,6 +573,274 @@ static void test_greedy_sample() {
     TEST(tok.cpu()[1].value == 1u);
 }
 
+// ------------------------------------------------------------------ training
+// Known answers of example/tests.h: mse :221-263, cross entropy :265-399,
+// softmax :619-679, adam :681-730, sgd :1109-1135, relu :1137-1167, scale
+// :1199-1222, embed backward :1224-1272, position add :1274-1316, rope
+// backward :1318-1385, sum_batch :1387-1409, rms_norm backward :1411-1470.
+static void set_values(Tensor& t, const std::vector<float>& v) { upload(t, v); }
+
+static void test_training_ops() {
+    std::printf("test_training_ops()\n");
+    {
+        Tensor p({3}), t({3}), g({3}), r({1});
+        set_values(p, {1, 2, 3});
+        set_values(t, {1, 2, 4});
+        evk::ai::mse_loss(p, t, g, r);
+        TEST(near(float(r.item()), 1.0f / 3.0f, 1e-3f));
+        std::vector<float> gv = download(g);
+        TEST(near(gv[0], 0, 5e-4f) && near(gv[1], 0, 5e-4f) && near(gv[2], -2.0f / 3.0f, 5e-3f));
+    }
+    {
+        Tensor logits({3, 4}), targets({3}), grad({3, 4}), loss({1});
+        set_values(logits, {0, 0, 0, 0, 0, 0, 2, 0, 1, -1, 0.5f, 0});
+        float16_t* tp = targets.cpu();
+        tp[0].value = 1;
+        tp[1].value = 3;
+        tp[2].value = 0;  // ignored
+        targets.cpu_upload();
+        evk::ai::cross_entropy_loss(logits, targets, grad, loss);
+        std::vector<float> g = download(grad);
+        const float e2 = std::exp(2.0f), den1 = 3.0f + e2;
+        const float want_loss = 0.5f * (std::log(4.0f) + (std::log(den1) - 0.0f));
+        TEST(near(float(loss.item()), want_loss, 5e-3f));
+        TEST(near(g[0], 0.125f, 1e-2f) && near(g[1], 0.125f - 0.5f, 1e-2f));
+        TEST(near(g[4 + 2], 0.5f * e2 / den1, 1e-2f) && near(g[4 + 3], 0.5f * (1.0f / den1 - 1.0f), 1e-2f));
+        TEST(g[8] == 0 && g[9] == 0 && g[10] == 0 && g[11] == 0);
+    }
+    {
+        Tensor in({1, 4}), out({1, 4});
+        set_values(in, {0, -65504, 1, -65504});
+        evk::ai::softmax(in, out, 1e-5f);
+        std::vector<float> p = download(out);
+        TEST(p[1] == 0 && p[3] == 0 && near(p[0] + p[2], 1.0f, 5e-3f) && p[0] > 0.49f && p[2] > 0.49f);
+    }
+    {
+        Tensor p({4}), g({4});
+        set_values(p, {1, -2, 0.5f, 4});
+        set_values(g, {0.5f, -1, 2, 0});
+        evk::ai::sgd(p, g, 0.1f);
+        std::vector<float> v = download(p);
+        TEST(near(v[0], 0.95f, 2e-2f) && near(v[1], -1.9f, 2e-2f) && near(v[2], 0.3f, 2e-2f) && v[3] == 4.0f);
+    }
+    {
+        Tensor x({4}), y({4}), go({4}), gi({4});
+        set_values(x, {-2, 0, 1.5f, 3});
+        evk::ai::relu(x, y);
+        go.fill(float16_t(1.0f));
+        gi.fill(float16_t(0.0f));
+        evk::ai::relu_backward(go, x, gi);
+        std::vector<float> yv = download(y), gv = download(gi);
+        TEST(yv[0] == 0 && yv[1] == 0 && yv[2] == 1.5f && yv[3] == 3.0f);
+        TEST(gv[0] == 0 && gv[1] == 0 && gv[2] == 1 && gv[3] == 1);
+        evk::ai::scale(x, 0.5f);
+        std::vector<float> sv = download(x);
+        TEST(sv[0] == -1 && sv[1] == 0 && sv[2] == 0.75f && sv[3] == 1.5f);
+    }
+    {
+        Tensor go({2, 3}), idx({2}), ge({4, 3});
+        set_values(go, {1, 2, 3, 4, 5, 6});
+        float16_t* ip = idx.cpu();
+        ip[0].value = 1;
+        ip[1].value = 3;
+        idx.cpu_upload();
+        ge.fill(float16_t(0.0f));
+        evk::ai::embed_backward(go, idx, ge);
+        std::vector<float> v = download(ge);
+        TEST(v[3] == 1 && v[4] == 2 && v[5] == 3 && v[9] == 4 && v[10] == 5 && v[11] == 6 && v[0] == 0 && v[6] == 0);
+    }
+    {
+        Tensor in({2, 2, 3}), pos({2, 3}), out({2, 2, 3}), go({2, 2, 3}), gi({2, 2, 3}), gp({2, 3});
+        in.fill(float16_t(0.0f));
+        set_values(pos, {1, 2, 3, 4, 5, 6});
+        evk::ai::position_add(in, pos, out, 2, 2, 3);
+        std::vector<float> o = download(out);
+        TEST(o[0] == 1 && o[5] == 6 && o[6] == 1 && o[11] == 6);
+        go.fill(float16_t(1.0f));
+        gi.fill(float16_t(0.0f));
+        gp.fill(float16_t(0.0f));
+        evk::ai::position_add_backward(go, gi, gp, 2, 2, 3);
+        std::vector<float> a = download(gi), b = download(gp);
+        bool ok = true;
+        for (float v : a) ok &= v == 1.0f;
+        for (float v : b) ok &= v == 2.0f;
+        TEST(ok);
+    }
+    {
+        Tensor go({1, 2, 4}), gi({1, 2, 4});
+        const std::vector<float> g = {1, 0, 1, 0, 0, 1, 0, 1};
+        set_values(go, g);
+        gi.fill(float16_t(0.0f));
+        evk::ai::rope_backward(go, gi, 1, 2, 4, 10000.0f);
+        std::vector<float> v = download(gi);
+        bool ok = true;
+        for (uint32_t t = 0; t < 2; ++t)
+            for (uint32_t pr = 0; pr < 2; ++pr) {
+                const uint32_t i = t * 4 + pr * 2;
+                const float a = float(t) * std::pow(10000.0f, -2.0f * float(pr) / 4.0f);
+                ok &= near(v[i], g[i] * std::cos(a) + g[i + 1] * std::sin(a), 3e-2f);
+                ok &= near(v[i + 1], -g[i] * std::sin(a) + g[i + 1] * std::cos(a), 3e-2f);
+            }
+        TEST(ok);
+    }
+    {
+        Tensor in({2, 3}), out({3});
+        set_values(in, {1, 2, 3, 4, 5, 6});
+        out.fill(float16_t(1.0f));
+        evk::ai::sum_batch(in, out, 2, 3);
+        std::vector<float> v = download(out);
+        TEST(v[0] == 6 && v[1] == 8 && v[2] == 10);
+    }
+    {
+        Tensor x({2, 4}), go({2, 4}), gi({2, 4});
+        const std::vector<float> xv = {3, 4, 0, 0, 1, 2, 3, 4};
+        set_values(x, xv);
+        go.fill(float16_t(1.0f));
+        gi.fill(float16_t(0.0f));
+        evk::ai::rms_norm_backward(x, go, gi, 1e-4f);
+        std::vector<float> v = download(gi);
+        bool ok = true;
+        for (uint32_t r = 0; r < 2; ++r) {
+            float ss = 0, dot = 0;
+            for (uint32_t d = 0; d < 4; ++d) ss += xv[r * 4 + d] * xv[r * 4 + d];
+            const float rms = std::sqrt(ss / 4 + 1e-4f);
+            for (uint32_t d = 0; d < 4; ++d) dot += xv[r * 4 + d] / rms;
+            for (uint32_t d = 0; d < 4; ++d)
+                ok &= near(v[r * 4 + d], 1 / rms - xv[r * 4 + d] / (rms * rms) * dot / 4, 4e-2f);
+        }
+        TEST(ok);
+    }
+    {
+        Tensor p({4}), g({4});
+        set_values(p, {1, 2, 3, 4});
+        set_values(g, {0.1f, 0.2f, 0.3f, 0.4f});
+        evk::ai::AdamState st;
+        for (int i = 0; i < 10; ++i) evk::ai::adam(p, g, st, 0.1f, 0.9f, 0.999f, 1e-4f);
+        std::vector<float> v = download(p);
+        TEST(v[0] < 1 && v[1] < 2 && v[2] < 3 && v[3] < 4);
+        TEST(st.t == 10);
+    }
+}
+
+// tests.h:565-591: y = W x + b fitted to 3 I by mse, 100 SGD steps; the loss
+// never rises (SGD's steps are mostly below half an fp16 ulp of the weights,
+// so that is all it can show).  Then the same with Adam, whose normalised
+// steps must at least halve the loss.
+static void test_graph_regression() {
+    std::printf("test_graph_regression()\n");
+    for (int use_adam = 0; use_adam < 2; ++use_adam) {
+        Graph graph;
+        const uint32_t n = 80;
+        Tensor& target = graph.tensor({n, n}).identity(3.0f);
+        Tensor& x = graph.tensor({n, n}).identity(1.0f);
+        Tensor& w = graph.tensor({n, n}, true).identity(1.0f);
+        Tensor& b = graph.tensor({n, n}, true).identity(1.0f);
+        Tensor& y = graph.add(graph.matmul(w, x), b);
+        Tensor& loss = graph.mse_loss(y, target);
+        float last = 1e9f, first = 0.0f;
+        bool monotone = true;
+        for (int i = 0; i < 100; ++i) {
+            graph.eval(true);
+            if (use_adam) graph.step_adam(0.01f);
+            else graph.step(0.05f);
+            const float l = float(loss.item());
+            if (i == 0) first = l;
+            monotone &= use_adam ? std::isfinite(l) : l <= last;
+            last = l;
+        }
+        TEST(monotone);
+        if (use_adam) TEST(last < 0.5f * first);
+    }
+}
+
+// Graph::causal_attention (fused causal flash attention) against the
+// reference's unfused matmul / mask / softmax / matmul composition on the
+// same inputs: output and the gradients of q, k and v.
+static void test_graph_causal_attention_fused_vs_unfused() {
+    std::printf("test_graph_causal_attention_fused_vs_unfused()\n");
+    const uint32_t B = 2, N = 48, D = 64;
+    Graph fused, plain;
+    std::vector<float> qv = random_vec(B * N * D, 91), kv = random_vec(B * N * D, 92), vv = random_vec(B * N * D, 93);
+    std::vector<float> gv = random_vec(B * N * D, 94);
+    Tensor* in_f[3];
+    Tensor* in_p[3];
+    for (int i = 0; i < 3; ++i) {
+        in_f[i] = &fused.tensor({B, N, D}, true);
+        in_p[i] = &plain.tensor({B, N, D}, true);
+        const std::vector<float>& src = i == 0 ? qv : i == 1 ? kv : vv;
+        upload(*in_f[i], src);
+        upload(*in_p[i], src);
+    }
+    Tensor& of = fused.causal_attention(*in_f[0], *in_f[1], *in_f[2]);
+    Tensor& op = plain.causal_attention_unfused(*in_p[0], *in_p[1], *in_p[2]);
+    // the loss sum(out * G) drives out.grad = G: seed it through a matmul-free
+    // path by running forward, then setting the output gradient and backward
+    fused.eval(false);
+    plain.eval(false);
+    std::vector<float> yf = download(of), yp = download(op);
+    float err = 0;
+    for (size_t i = 0; i < yf.size(); ++i) err = std::fmax(err, std::fabs(yf[i] - yp[i]));
+    TEST(err < 2e-2f);
+    for (Graph* g : {&fused, &plain}) {
+        for (auto& nd : g->nodes) evk::ai::zero(nd->grad());
+    }
+    upload(of.grad(), gv);
+    upload(op.grad(), gv);
+    for (Graph* g : {&fused, &plain})
+        for (auto it = g->nodes.rbegin(); it != g->nodes.rend(); ++it)
+            if ((*it)->backward_fn) (*it)->backward_fn();
+    evk::ai::SubmitCmd(true);
+    bool ok = true;
+    for (int i = 0; i < 3; ++i) {
+        std::vector<float> a = download(in_f[i]->grad()), b = download(in_p[i]->grad());
+        float e = 0, m = 0;
+        for (size_t j = 0; j < a.size(); ++j) {
+            e = std::fmax(e, std::fabs(a[j] - b[j]));
+            m = std::fmax(m, std::fabs(b[j]));
+        }
+        ok &= e <= 2e-2f + 2e-2f * m;
+        std::printf("  grad %d: max |fused - unfused| %.4g (max |unfused| %.4g)\n", i, e, m);
+    }
+    TEST(ok);
+}
+
+// A one-block causal language model through the Graph: embed, rope, fused
+// causal attention over q = k = v projections, output projection, cross
+// entropy; 30 Adam steps on a fixed batch must lower the loss.
+static void test_graph_tiny_lm() {
+    std::printf("test_graph_tiny_lm()\n");
+    const uint32_t B = 2, N = 32, D = 64, V = 96;
+    Graph g;
+    Tensor& E = g.tensor({V, D}, true).random_init(0.1f);
+    Tensor& Wq = g.tensor({D, D}, true).random_init(0.1f);
+    Tensor& Wk = g.tensor({D, D}, true).random_init(0.1f);
+    Tensor& Wv = g.tensor({D, D}, true).random_init(0.1f);
+    Tensor& Wo = g.tensor({D, V}, true).random_init(0.1f);
+    Tensor& ids = g.tensor({B, N});
+    Tensor& tgt = g.tensor({B, N});
+    float16_t* ip = ids.cpu();
+    float16_t* tp = tgt.cpu();
+    for (uint32_t i = 0; i < B * N; ++i) {
+        ip[i].value = uint16_t(1 + (i * 7) % (V - 1));
+        tp[i].value = uint16_t(1 + (i * 7 + 7) % (V - 1));  // next token of the pattern
+    }
+    ids.cpu_upload();
+    tgt.cpu_upload();
+    Tensor& x = g.rms_norm(g.rope(g.embed(E, ids)));
+    Tensor& att = g.causal_attention(g.matmul(x, Wq), g.matmul(x, Wk), g.matmul(x, Wv));
+    Tensor& h = g.residual(x, att);
+    Tensor& loss = g.cross_entropy_loss(g.matmul(h, Wo), tgt);
+    float first = 0, last = 0;
+    for (int step = 0; step < 30; ++step) {
+        g.eval(true);
+        g.step_adam(3e-2f);
+        last = float(loss.item());
+        if (step == 0) first = last;
+    }
+    std::printf("  loss %.4f -> %.4f\n", first, last);
+    TEST(std::isfinite(last) && last < 0.7f * first);
+}
+
 static void test_timestamps() {
     std::printf("test_timestamps()\n");
     const uint32_t n = 1024;
@@ -649,6 +917,10 @@ int main(int argc, char** argv) {
     test_rope();
     test_rms_norm();
     test_greedy_sample();
+    test_training_ops();
+    test_graph_regression();
+    test_graph_causal_attention_fused_vs_unfused();
+    test_graph_tiny_lm();
     test_timestamps();
     evk::ai::shutdown();
     std::printf("ALL PASSED\n");
