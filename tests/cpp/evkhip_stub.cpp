@@ -8,6 +8,7 @@
 namespace {
 StubCall g_last;
 int g_count = 0;
+std::vector<std::string> g_log;
 int g_fail_status = 0;
 std::string g_fail_msg, g_error;
 
@@ -20,6 +21,7 @@ uint64_t elems(const evkhip_tensor* t) {
 int record(const char* name, std::initializer_list<const evkhip_tensor*> ts, std::initializer_list<long long> ints,
            std::initializer_list<double> floats, void* stream, const void* ptr = nullptr) {
     ++g_count;
+    g_log.push_back(name);
     g_last = StubCall{};
     g_last.name = name;
     for (const evkhip_tensor* t : ts) {
@@ -45,6 +47,12 @@ const StubCall& stub_last_call() {
 }
 int stub_call_count() {
     return g_count;
+}
+const std::vector<std::string>& stub_call_log() {
+    return g_log;
+}
+void stub_clear_log() {
+    g_log.clear();
 }
 void stub_fail_next(int status, const char* msg) {
     g_fail_status = status;
@@ -93,6 +101,66 @@ int evkhip_rope(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t b, u
 }
 int evkhip_gelu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream) {
     return record("gelu", {in, out}, {}, {}, stream);
+}
+// training ops: recorded only
+int evkhip_scale(const evkhip_tensor* t, float factor, void* stream) {
+    return record("scale", {t}, {}, {factor}, stream);
+}
+int evkhip_relu(const evkhip_tensor* in, const evkhip_tensor* out, void* stream) {
+    return record("relu", {in, out}, {}, {}, stream);
+}
+int evkhip_relu_backward(const evkhip_tensor* go, const evkhip_tensor* in, const evkhip_tensor* gi, void* stream) {
+    return record("relu_backward", {go, in, gi}, {}, {}, stream);
+}
+int evkhip_gelu_backward(const evkhip_tensor* go, const evkhip_tensor* in, const evkhip_tensor* gi, void* stream) {
+    return record("gelu_backward", {go, in, gi}, {}, {}, stream);
+}
+int evkhip_mse_loss(const evkhip_tensor* p, const evkhip_tensor* t, const evkhip_tensor* g, const evkhip_tensor* r,
+                    void* stream) {
+    return record("mse_loss", {p, t, g, r}, {}, {}, stream);
+}
+int evkhip_sgd(const evkhip_tensor* p, const evkhip_tensor* g, float lr, void* stream) {
+    return record("sgd", {p, g}, {}, {lr}, stream);
+}
+int evkhip_adam(const evkhip_tensor* p, const evkhip_tensor* g, const evkhip_tensor* m, const evkhip_tensor* v,
+                float lr, float b1, float b2, float c1, float c2, float eps, void* stream) {
+    return record("adam", {p, g, m, v}, {}, {lr, b1, b2, c1, c2, eps}, stream);
+}
+int evkhip_softmax(const evkhip_tensor* in, const evkhip_tensor* out, float scale, void* stream) {
+    return record("softmax", {in, out}, {}, {scale}, stream);
+}
+int evkhip_softmax_backward(const evkhip_tensor* p, const evkhip_tensor* go, const evkhip_tensor* gi, float scale,
+                            void* stream) {
+    return record("softmax_backward", {p, go, gi}, {}, {scale}, stream);
+}
+int evkhip_rms_norm_backward(const evkhip_tensor* in, const evkhip_tensor* go, const evkhip_tensor* gi, float eps,
+                             void* stream) {
+    return record("rms_norm_backward", {in, go, gi}, {}, {eps}, stream);
+}
+int evkhip_cross_entropy_loss(const evkhip_tensor* l, const evkhip_tensor* t, const evkhip_tensor* g,
+                              const evkhip_tensor* r, void* stream) {
+    return record("cross_entropy_loss", {l, t, g, r}, {}, {}, stream);
+}
+int evkhip_sum_batch(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t b, uint32_t n, void* stream) {
+    return record("sum_batch", {in, out}, {b, n}, {}, stream);
+}
+int evkhip_apply_causal_mask(const evkhip_tensor* s, void* stream) {
+    return record("apply_causal_mask", {s}, {}, {}, stream);
+}
+int evkhip_position_add(const evkhip_tensor* in, const evkhip_tensor* pos, const evkhip_tensor* out, uint32_t b,
+                        uint32_t n, uint32_t d, void* stream) {
+    return record("position_add", {in, pos, out}, {b, n, d}, {}, stream);
+}
+int evkhip_position_add_backward(const evkhip_tensor* go, const evkhip_tensor* gi, const evkhip_tensor* gp,
+                                 uint32_t b, uint32_t n, uint32_t d, void* stream) {
+    return record("position_add_backward", {go, gi, gp}, {b, n, d}, {}, stream);
+}
+int evkhip_rope_backward(const evkhip_tensor* go, const evkhip_tensor* gi, uint32_t b, uint32_t n, uint32_t d,
+                         float base, void* stream) {
+    return record("rope_backward", {go, gi}, {b, n, d}, {base}, stream);
+}
+int evkhip_embed_backward(const evkhip_tensor* go, const evkhip_tensor* idx, const evkhip_tensor* ge, void* stream) {
+    return record("embed_backward", {go, idx, ge}, {}, {}, stream);
 }
 // add is computed (fp32 sum rounded to fp16) so data round trips can be checked
 int evkhip_add(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, void* stream) {

@@ -20,6 +20,9 @@ struct StubCall {
 
 const StubCall& stub_last_call();
 int stub_call_count();
+// Names of the entry points called since the last stub_clear_log(), in order.
+const std::vector<std::string>& stub_call_log();
+void stub_clear_log();
 // The next entry point call returns `status` (once) with message `msg`.
 void stub_fail_next(int status, const char* msg);
 

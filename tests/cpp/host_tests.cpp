@@ -254,6 +254,56 @@ static void test_op_marshalling() {
     TEST(mock_errors() == 0);
 }
 
+// AdamState bookkeeping and the Graph's call order, against the recording
+// stub: bias corrections from the step count, the forward functions in
+// order and the backward ones in reverse, causal_attention on the fused
+// flash entry points (the unfused chain only for a non-default scale).
+static void test_training_host() {
+    std::printf("test_training_host()\n");
+    Tensor p({40}), g({40});
+    evk::ai::AdamState st;
+    evk::ai::adam(p, g, st, 0.01f, 0.9f, 0.999f, 1e-4f);
+    evk::ai::adam(p, g, st, 0.01f, 0.9f, 0.999f, 1e-4f);
+    const StubCall& a = stub_last_call();
+    TEST(a.name == "adam" && st.t == 2 && bool(st.m_buffer) && bool(st.v_buffer));
+    TEST(a.tensors.size() == 4 && a.tensors[2].dims[0] == 40 && a.tensors[3].dims[0] == 40);
+    const double c1 = 1.0 / (1.0 - 0.9 * 0.9), c2 = 1.0 / (1.0 - 0.999 * 0.999);
+    TEST(std::fabs(a.floats[3] - c1) < 1e-4 * c1 && std::fabs(a.floats[4] - c2) < 1e-3 * c2);
+    st.reset();
+    TEST(!st.m_buffer && st.t == 0);
+
+    Graph gr;
+    Tensor& x = gr.tensor({8, 8});
+    Tensor& w = gr.tensor({8, 8}, true);
+    Tensor& tgt = gr.tensor({8, 8});
+    Tensor& loss = gr.mse_loss(gr.relu(gr.matmul(w, x)), tgt);
+    (void)loss;
+    stub_clear_log();
+    gr.eval(true);
+    gr.step(0.1f);
+    const std::vector<std::string> want = {"matmul", "relu", "mse_loss", "relu_backward", "matmul", "matmul", "sgd"};
+    TEST(stub_call_log() == want);
+
+    Graph ga;
+    Tensor& q = ga.tensor({2, 16, 32}, true);
+    Tensor& k = ga.tensor({2, 16, 32}, true);
+    Tensor& v = ga.tensor({2, 16, 32}, true);
+    ga.causal_attention(q, k, v);
+    stub_clear_log();
+    ga.eval(true);
+    const std::vector<std::string> fused = {"flash_attention", "flash_attention_bwd", "add", "add", "add"};
+    TEST(stub_call_log() == fused);
+    Graph gu;
+    Tensor& q2 = gu.tensor({2, 16, 32}, true);
+    gu.causal_attention(q2, q2, q2, 0.5f);
+    stub_clear_log();
+    gu.eval(false);
+    const std::vector<std::string> unfused = {"matmul", "apply_causal_mask", "softmax", "matmul"};
+    TEST(stub_call_log() == unfused);
+    evk::ai::SubmitCmd(true);
+    TEST(mock_errors() == 0);
+}
+
 int main() {
     std::setvbuf(stdout, nullptr, _IONBF, 0);
     test_uninitialized_use_aborts();
@@ -268,6 +318,7 @@ int main() {
     test_submissions_and_timestamps();
     test_tensor_host_paths();
     test_op_marshalling();
+    test_training_host();
     evk::ai::shutdown();
     TEST(!evk::IsInitialized());
     TEST(mock_live_allocations() == 0);
