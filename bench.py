@@ -251,6 +251,71 @@ def main():
                             "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
                             "bytes_per_token": int(step_bytes)}
         del w, cache
+    if want("train"):
+        # training ops (HBM-bound) and the Graph's causal attention, fused
+        # flash against the reference's unfused chain
+        n_p = 64 << 20
+        prm = to_dev(orc.uniform_f16((n_p,), 601))
+        grd = to_dev(orc.normal_f16((n_p,), 602))
+        m_s = torch.zeros(n_p, dtype=torch.float16, device=dev)
+        v_s = torch.zeros(n_p, dtype=torch.float16, device=dev)
+        # in-place state: no bit-equality check between replays
+        ms_ = timed(lambda: evk.adam(prm, grd, m_s, v_s, 1e-3, 0.9, 0.999, 10.0, 1000.0, 1e-4), 20, 3)
+        gbs = 14.0 * n_p / (ms_ * 1e-3) / 1e9
+        sec["train_adam_64M"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
+                                 "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        del prm, grd, m_s, v_s
+        P_, V_ = 8192, 32000
+        lg = to_dev(orc.normal_f16((P_, V_), 603))
+        tg = torch.from_numpy(orc.tokens_u16(P_, 604, V_).view(np.int16)).to(dev)
+        gr = torch.empty_like(lg)
+        ls = torch.empty(1, dtype=torch.float16, device=dev)
+        ms_ = timed(lambda: evk.cross_entropy_loss(lg, tg, gr, ls), 20, 3, check=lambda: (gr, ls))
+        gbs = 4.0 * P_ * V_ / (ms_ * 1e-3) / 1e9
+        sec["train_cross_entropy_8192x32000"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
+                                                 "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        del lg, gr
+        sm_in = to_dev(orc.normal_f16((32, 1024, 1024), 605))
+        sm_out = torch.empty_like(sm_in)
+        ms_ = timed(lambda: evk.softmax(sm_in, sm_out, 0.125), 50, 5, check=lambda: (sm_out,))
+        gbs = 4.0 * sm_in.numel() / (ms_ * 1e-3) / 1e9
+        sec["train_softmax_32x1024x1024"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
+                                             "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        del sm_in, sm_out
+        Bq, Nq, Dq = 4, 1024, 64
+        qa = to_dev(orc.normal_f16((Bq, Nq, Dq), 606))
+        ka = to_dev(orc.normal_f16((Bq, Nq, Dq), 607))
+        va = to_dev(orc.normal_f16((Bq, Nq, Dq), 608))
+        ga = to_dev(orc.normal_f16((Bq, Nq, Dq), 609))
+        oa, la = torch.empty_like(qa), torch.empty((Bq, 1, Nq), dtype=torch.float32, device=dev)
+        dqa, dka, dva = torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+
+        def fused():
+            evk.flash_attention(qa, ka, va, oa, causal=True, lse=la)
+            evk.flash_attention_bwd(qa, ka, va, oa, ga, dqa, dka, dva, heads=1, causal=True, lse=la)
+
+        ms_f = timed(fused, 50, 5, check=lambda: (oa, dqa, dka, dva))
+        sc_ = torch.empty((Bq, Nq, Nq), dtype=torch.float16, device=dev)
+        pr_, dp_, ds_ = torch.empty_like(sc_), torch.empty_like(sc_), torch.empty_like(sc_)
+        ou_, dqu, dku, dvu = torch.empty_like(qa), torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+
+        def unfused():  # Graph::causal_attention of the reference (evk_ai.h:961-1007)
+            evk.matmul(qa, ka, sc_, False, True)
+            evk.apply_causal_mask(sc_)
+            evk.softmax(sc_, pr_, 0.125)
+            evk.matmul(pr_, va, ou_)
+            evk.matmul(ga, va, dp_, False, True)
+            evk.matmul(pr_, ga, dvu, True, False)
+            ds_.zero_()
+            evk.softmax_backward(pr_, dp_, ds_, 0.125)
+            evk.matmul(ds_, ka, dqu)
+            evk.matmul(ds_, qa, dku, True, False)
+
+        ms_u = timed(unfused, 20, 3, check=lambda: (ou_, dqu, dku, dvu))
+        sec["graph_causal_attention_4x1024x64_fwd_bwd"] = {
+            "fused_flash_ms": round(ms_f, 4), "unfused_ms": round(ms_u, 4),
+            "speedup": round(ms_u / ms_f, 2)}
+        del qa, ka, va, ga, oa, dqa, dka, dva, sc_, pr_, dp_, ds_, ou_, dqu, dku, dvu
     if sec:
         out["secondary"] = sec
 

@@ -396,7 +396,7 @@ int evkhip_adam(const evkhip_tensor* param, const evkhip_tensor* gradient, const
                   "adam: state must hold one value per parameter");
     return adam_launch((f16*)param->data, (const f16*)gradient->data, (f16*)m_state->data, (f16*)v_state->data,
                        (int64_t)n, learning_rate, beta1, beta2, beta1_correction_inv, beta2_correction_inv, epsilon,
-                       as_stream(stream));
+                       all_aligned({param, gradient, m_state, v_state}), as_stream(stream));
 }
 
 int evkhip_softmax(const evkhip_tensor* in, const evkhip_tensor* out, float input_scale, void* stream) {
@@ -406,7 +406,7 @@ int evkhip_softmax(const evkhip_tensor* in, const evkhip_tensor* out, float inpu
     const uint32_t D = dim_at(in, -1);
     if (D == 0) return EVKHIP_OK;
     return softmax_launch((const f16*)in->data, (f16*)out->data, input_scale, (int)D, (int64_t)(numel(in) / D),
-                          as_stream(stream));
+                          all_aligned({in, out}), as_stream(stream));
 }
 
 int evkhip_softmax_backward(const evkhip_tensor* probs, const evkhip_tensor* grad_out,
@@ -447,7 +447,8 @@ int evkhip_cross_entropy_loss(const evkhip_tensor* logits, const evkhip_tensor* 
     EVK_RETURN_IF(result->dims[0] != 1, EVKHIP_ERR_SHAPE, "cross_entropy_loss: result must be (1)");
     EVK_RETURN_IF(V == 0 && P > 0, EVKHIP_ERR_SHAPE, "cross_entropy_loss: empty vocabulary");
     return cross_entropy_launch((const f16*)logits->data, (const uint16_t*)targets->data, (f16*)grad->data,
-                                (f16*)result->data, (int64_t)P, (int)V, as_stream(stream));
+                                (f16*)result->data, (int64_t)P, (int)V, all_aligned({logits, grad}),
+                                as_stream(stream));
 }
 
 int evkhip_sum_batch(const evkhip_tensor* in, const evkhip_tensor* out, uint32_t batch_count,

@@ -58,14 +58,14 @@ int relu_bwd_launch(const f16* gout, const f16* in, f16* gin, int64_t n, bool ve
 int gelu_bwd_launch(const f16* gout, const f16* in, f16* gin, int64_t n, bool vec, hipStream_t st);
 int sgd_launch(f16* param, const f16* grad, float lr, int64_t n, bool vec, hipStream_t st);
 int adam_launch(f16* param, const f16* grad, f16* m, f16* v, int64_t n, float lr, float beta1, float beta2,
-                float c1inv, float c2inv, float eps, hipStream_t st);
-int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, hipStream_t st);
+                float c1inv, float c2inv, float eps, bool vec, hipStream_t st);
+int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, bool vec, hipStream_t st);
 int softmax_bwd_launch(const f16* probs, const f16* gout, f16* gin, float scale, int D, int64_t rows,
                        hipStream_t st);
 int rms_norm_bwd_launch(const f16* in, const f16* gout, f16* gin, float eps, int D, int64_t rows, hipStream_t st);
 int mse_loss_launch(const f16* pred, const f16* tgt, f16* grad, f16* result, int64_t n, hipStream_t st);
 int cross_entropy_launch(const f16* logits, const uint16_t* tgt, f16* grad, f16* result, int64_t rows, int V,
-                         hipStream_t st);
+                         bool vec, hipStream_t st);
 int sum_batch_launch(const f16* in, f16* out, int batch, int64_t per_batch, hipStream_t st);
 int causal_mask_launch(f16* scores, int64_t batch, int N, hipStream_t st);
 int position_add_launch(const f16* in, const f16* pos, f16* out, int B, int64_t per_batch, hipStream_t st);

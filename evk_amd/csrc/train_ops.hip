@@ -128,25 +128,38 @@ struct AdamArgs {
     f16* v;
     float lr, beta1, beta2, c1inv, c2inv, eps;
 };
-__global__ __launch_bounds__(EW_NT) void adam_k(AdamArgs a, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * EW_NT + threadIdx.x;
-    if (i >= n) return;
+// one element; returns false when the gradient is not finite (nothing changes)
+DEV void adam_one(const AdamArgs& a, float g, float& p, float& mq, float& vq) {
     const float kOffset = 41.0f, kMinRms = 1.0e-12f;
-    const float g = hf(a.grad[i]);
     if (!isfinite(g)) return;
-    const float stored = hf(a.v[i]);
-    float rms = stored > 0.0f ? exp2f(stored - kOffset) : 0.0f;
-    float m = hf(a.m[i]) * rms;
+    float rms = vq > 0.0f ? exp2f(vq - kOffset) : 0.0f;
+    float m = mq * rms;
     float v = rms * rms;
     m = a.beta1 * m + (1.0f - a.beta1) * g;
     v = a.beta2 * v + (1.0f - a.beta2) * g * g;
     rms = sqrtf(fmaxf(v, 0.0f));
     const float m_norm = m / fmaxf(rms, 1.0e-8f);
-    if (isfinite(m_norm)) a.m[i] = (f16)m_norm;
+    if (isfinite(m_norm)) mq = m_norm;
     const float log_rms = log2f(fmaxf(rms, kMinRms)) + kOffset;
-    if (isfinite(log_rms)) a.v[i] = (f16)log_rms;
+    if (isfinite(log_rms)) vq = log_rms;
     const float upd = a.lr * (m * a.c1inv) / (rms * sqrtf(a.c2inv) + a.eps);
-    if (isfinite(upd)) a.param[i] = (f16)fminf(fmaxf(hf(a.param[i]) - upd, -65504.0f), 65504.0f);
+    if (isfinite(upd)) p = fminf(fmaxf(p - upd, -65504.0f), 65504.0f);
+}
+// 8 elements per thread; a value that is not updated is stored back as it
+// was read (its fp16 bits round-trip exactly)
+__global__ __launch_bounds__(EW_NT) void adam_k(AdamArgs a, int64_t n, bool vec) {
+    const int64_t i0 = first8();
+    if (i0 >= n) return;
+    float p[8], g[8], m[8], v[8];
+    ld8(a.param, i0, n, vec, p);
+    ld8(a.grad, i0, n, vec, g);
+    ld8(a.m, i0, n, vec, m);
+    ld8(a.v, i0, n, vec, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) adam_one(a, g[e], p[e], m[e], v[e]);
+    st8(a.param, i0, n, vec, p);
+    st8(a.m, i0, n, vec, m);
+    st8(a.v, i0, n, vec, v);
 }
 
 // position_add.comp: out[b, t, d] = fp16(in[b, t, d] + pos[t, d])
@@ -249,6 +262,58 @@ __global__ __launch_bounds__(EW_NT) void softmax_k(const f16* in, f16* out, floa
     for (int j = lane; j < D; j += 64) {
         const float r = hf(x[j]);
         y[j] = (f16)(r > kMask ? expf(r * scale - mx) * inv : 0.0f);
+    }
+}
+
+// softmax.comp with the row in registers: D % 8 == 0, 16-byte aligned rows,
+// D <= 64 * 8 * NV; one HBM read and one write per element
+template <int NV>
+__global__ __launch_bounds__(EW_NT) void softmax_reg_k(const f16* in, f16* out, float scale, int D, int64_t rows) {
+    const int64_t row = (int64_t)blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const half8* x = reinterpret_cast<const half8*>(in + row * D);
+    half8* y = reinterpret_cast<half8*>(out + row * D);
+    const int nc = D / 8;  // 16-byte chunks of the row
+    const float kMask = -65504.0f;
+    half8 r[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int c = lane + 64 * u;
+        if (c < nc) r[u] = x[c];
+    }
+    float mx = -3.402823466e+38f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        if (lane + 64 * u < nc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = (float)r[u][e];
+                if (v > kMask) mx = fmaxf(mx, v * scale);
+            }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        if (lane + 64 * u < nc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = (float)r[u][e];
+                if (v > kMask) sum += expf(v * scale - mx);
+            }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / fmaxf(sum, 1e-20f);
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int c = lane + 64 * u;
+        if (c >= nc) continue;
+        half8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = (float)r[u][e];
+            o[e] = (f16)(v > kMask ? expf(v * scale - mx) * inv : 0.0f);
+        }
+        y[c] = o;
     }
 }
 
@@ -385,6 +450,77 @@ __global__ __launch_bounds__(CE_NT) void ce_row_k(const f16* logits, const uint1
     if (threadIdx.x == 0) ws[1 + row] = ((mx + log_sum) - lv(t)) * inv_valid;
 }
 
+// ce_row_k with the row in registers: V % 8 == 0, 16-byte aligned rows,
+// V <= CE_NT * 8 * NV; one HBM read and one write per logit
+template <int NV>
+__global__ __launch_bounds__(CE_NT) void ce_row_reg_k(const f16* logits, const uint16_t* tgt, f16* grad, float* ws,
+                                                      int V) {
+    __shared__ float sh[2 * (CE_NT / 64)];
+    const int64_t row = blockIdx.x;
+    const half8* x = reinterpret_cast<const half8*>(logits + row * V);
+    half8* g = reinterpret_cast<half8*>(grad + row * V);
+    const int nc = V / 8;
+    const int t = tgt[row];
+    const float n_valid = ws[0];
+    const bool valid = t != 0 && t < V && n_valid > 0.0f;
+    if (!valid) {
+        const half8 z = {};
+        for (int c = threadIdx.x; c < nc; c += CE_NT) g[c] = z;
+        if (threadIdx.x == 0) ws[1 + row] = 0.0f;
+        return;
+    }
+    half8 r[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int c = threadIdx.x + CE_NT * u;
+        if (c < nc) r[u] = x[c];
+    }
+    auto cl = [](f16 h) { return fminf(fmaxf((float)h, -65000.0f), 65000.0f); };
+    float mx = -3.402823466e+38f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        if (threadIdx.x + CE_NT * u < nc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, cl(r[u][e]));
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = sh[0];
+#pragma unroll
+    for (int w = 1; w < CE_NT / 64; ++w) mx = fmaxf(mx, sh[w]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u)
+        if (threadIdx.x + CE_NT * u < nc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += expf(cl(r[u][e]) - mx);
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) sh[CE_NT / 64 + (threadIdx.x >> 6)] = sum;
+    __syncthreads();
+    sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < CE_NT / 64; ++w) sum += sh[CE_NT / 64 + w];
+    sum = fmaxf(sum, 1e-20f);
+    const float inv_valid = 1.0f / n_valid;
+    const float inv_sum = 1.0f / sum, log_sum = logf(sum);
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int c = threadIdx.x + CE_NT * u;
+        if (c >= nc) continue;
+        half8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float gv = expf(cl(r[u][e]) - mx) * inv_sum * inv_valid;
+            if (c * 8 + e == t) {
+                gv -= inv_valid;
+                ws[1 + row] = ((mx + log_sum) - cl(r[u][e])) * inv_valid;
+            }
+            o[e] = (f16)gv;
+        }
+        g[c] = o;
+    }
+}
+
 // cross_entropy_scale.comp: the mean loss (0 when nothing is valid or the
 // sum is not finite), summed over rows in a fixed order
 __global__ __launch_bounds__(RED_NT) void ce_final_k(const float* ws, f16* result, int64_t rows) {
@@ -445,14 +581,23 @@ int sgd_launch(f16* param, const f16* grad, float lr, int64_t n, bool vec, hipSt
     return launched("sgd launch");
 }
 int adam_launch(f16* param, const f16* grad, f16* m, f16* v, int64_t n, float lr, float beta1, float beta2,
-                float c1inv, float c2inv, float eps, hipStream_t st) {
+                float c1inv, float c2inv, float eps, bool vec, hipStream_t st) {
     if (n == 0) return EVKHIP_OK;
     AdamArgs a{param, grad, m, v, lr, beta1, beta2, c1inv, c2inv, eps};
-    hipLaunchKernelGGL(adam_k, dim3(ew_grid(n)), dim3(EW_NT), 0, st, a, n);
+    hipLaunchKernelGGL(adam_k, dim3(ew_grid8(n)), dim3(EW_NT), 0, st, a, n, vec);
     return launched("adam launch");
 }
-int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, hipStream_t st) {
+int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, bool vec, hipStream_t st) {
     if (rows == 0 || D == 0) return EVKHIP_OK;
+    if (vec && D % 8 == 0 && D <= 64 * 8 * 4) {
+        if (D <= 64 * 8)
+            hipLaunchKernelGGL(softmax_reg_k<1>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+        else if (D <= 64 * 8 * 2)
+            hipLaunchKernelGGL(softmax_reg_k<2>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+        else
+            hipLaunchKernelGGL(softmax_reg_k<4>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+        return launched("softmax launch");
+    }
     hipLaunchKernelGGL(softmax_k, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
     return launched("softmax launch");
 }
@@ -473,7 +618,7 @@ int mse_loss_launch(const f16* pred, const f16* tgt, f16* grad, f16* result, int
     return launched("mse_loss launch");
 }
 int cross_entropy_launch(const f16* logits, const uint16_t* tgt, f16* grad, f16* result, int64_t rows, int V,
-                         hipStream_t st) {
+                         bool vec, hipStream_t st) {
     if (rows == 0) {  // nothing valid: loss 0
         hipLaunchKernelGGL(ce_final_k, dim3(1), dim3(RED_NT), 0, st, (const float*)nullptr, result, (int64_t)0);
         return launched("cross_entropy launch");
@@ -487,7 +632,15 @@ int cross_entropy_launch(const f16* logits, const uint16_t* tgt, f16* grad, f16*
         g_ce_ws_n = need;
     }
     hipLaunchKernelGGL(ce_count_k, dim3(1), dim3(RED_NT), 0, st, tgt, g_ce_ws, rows, V);
-    hipLaunchKernelGGL(ce_row_k, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws, V);
+    if (vec && V % 8 == 0 && V <= CE_NT * 8 * 16) {
+        if (V <= CE_NT * 8 * 4)
+            hipLaunchKernelGGL(ce_row_reg_k<4>, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws, V);
+        else
+            hipLaunchKernelGGL(ce_row_reg_k<16>, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws,
+                               V);
+    } else {
+        hipLaunchKernelGGL(ce_row_k, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws, V);
+    }
     hipLaunchKernelGGL(ce_final_k, dim3(1), dim3(RED_NT), 0, st, (const float*)g_ce_ws, result, rows);
     return launched("cross_entropy launch");
 }

@@ -83,7 +83,8 @@ def test_adam_steps(dev, orc):
     assert_close_f16(from_dev(V), v, what="adam log2 rms")
 
 
-@pytest.mark.parametrize("shape,scale", [((3, 5), 1.0), ((2, 4, 129), 0.125), ((5, 1000), 1e-3), ((1, 1), 2.0)])
+@pytest.mark.parametrize("shape,scale", [((3, 5), 1.0), ((2, 4, 129), 0.125), ((5, 1000), 1e-3), ((1, 1), 2.0),
+                                         ((7, 8), 0.5), ((3, 2048), 0.25), ((2, 4096), 0.1)])
 def test_softmax_and_backward(dev, orc, shape, scale):
     import evk_amd as evk
     x = rnd(21, shape, 3)
@@ -125,7 +126,7 @@ def test_mse_loss(dev, orc, n):
     assert_close_f16(from_dev(R), wr, atol=1e-3, rtol=1e-3, what="mse loss")
 
 
-@pytest.mark.parametrize("P,V", [(3, 4), (17, 1000), (64, 32000), (5, 3)])
+@pytest.mark.parametrize("P,V", [(3, 4), (17, 1000), (64, 32000), (5, 3), (4, 32768), (3, 40000)])
 def test_cross_entropy(dev, orc, P, V):
     import torch
 
