@@ -38,7 +38,7 @@ def test_config2_causal_flash_forward(dev, orc, causal):
     assert np.abs(lse - wl).max() < 1e-2
 
 
-@pytest.mark.parametrize("Dh", [32, 64, 128, 16, 48])
+@pytest.mark.parametrize("Dh", [32, 64, 128, 16, 48, 96, 256])
 @pytest.mark.parametrize("N", [1, 33, 100, 130])
 def test_flash_forward_ragged_heads(dev, orc, Dh, N):
     import evk_amd as evk
@@ -105,7 +105,7 @@ def test_config3_causal_flash_backward(dev, orc, use_lse):
     assert_close_f16(dv, wv, what="dV")
 
 
-@pytest.mark.parametrize("Dh", [32, 64, 128, 16])
+@pytest.mark.parametrize("Dh", [32, 64, 128, 16, 256])
 @pytest.mark.parametrize("N", [16, 45, 96])
 def test_flash_backward_ragged(dev, orc, Dh, N):
     import evk_amd as evk
