@@ -265,55 +265,60 @@ __global__ __launch_bounds__(EW_NT) void softmax_k(const f16* in, f16* out, floa
     }
 }
 
-// softmax.comp with the row in registers: D % 8 == 0, 16-byte aligned rows,
-// D <= 64 * 8 * NV; one HBM read and one write per element
-template <int NV>
+// softmax.comp with rows in registers: D % 8 == 0, 16-byte aligned rows,
+// D <= 64 * 8 * NV.  A wave takes RPW rows and requests all of them before
+// any arithmetic; each exponential is formed once.  One HBM read and one
+// write per element.
+template <int NV, int RPW>
 __global__ __launch_bounds__(EW_NT) void softmax_reg_k(const f16* in, f16* out, float scale, int D, int64_t rows) {
-    const int64_t row = (int64_t)blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * ROWS_PER_WG + (threadIdx.x >> 6)) * RPW;
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const half8* x = reinterpret_cast<const half8*>(in + row * D);
-    half8* y = reinterpret_cast<half8*>(out + row * D);
-    const int nc = D / 8;  // 16-byte chunks of the row
+    if (row0 >= rows) return;
+    const int nc = D / 8;  // 16-byte chunks of a row
     const float kMask = -65504.0f;
-    half8 r[NV];
+    half8 r[RPW][NV];
 #pragma unroll
-    for (int u = 0; u < NV; ++u) {
-        const int c = lane + 64 * u;
-        if (c < nc) r[u] = x[c];
-    }
-    float mx = -3.402823466e+38f;
+    for (int k = 0; k < RPW; ++k)
 #pragma unroll
-    for (int u = 0; u < NV; ++u)
-        if (lane + 64 * u < nc)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float v = (float)r[u][e];
-                if (v > kMask) mx = fmaxf(mx, v * scale);
-            }
-    mx = wave_max(mx);
-    float sum = 0.0f;
-#pragma unroll
-    for (int u = 0; u < NV; ++u)
-        if (lane + 64 * u < nc)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float v = (float)r[u][e];
-                if (v > kMask) sum += expf(v * scale - mx);
-            }
-    sum = wave_sum(sum);
-    const float inv = 1.0f / fmaxf(sum, 1e-20f);
-#pragma unroll
-    for (int u = 0; u < NV; ++u) {
-        const int c = lane + 64 * u;
-        if (c >= nc) continue;
-        half8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float v = (float)r[u][e];
-            o[e] = (f16)(v > kMask ? expf(v * scale - mx) * inv : 0.0f);
+        for (int u = 0; u < NV; ++u) {
+            const int c = lane + 64 * u;
+            if (row0 + k < rows && c < nc) r[k][u] = reinterpret_cast<const half8*>(in + (row0 + k) * D)[c];
         }
-        y[c] = o;
+#pragma unroll
+    for (int k = 0; k < RPW; ++k) {
+        if (row0 + k >= rows) break;
+        float mx = -3.402823466e+38f;
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+            if (lane + 64 * u < nc)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = (float)r[k][u][e];
+                    if (v > kMask) mx = fmaxf(mx, v * scale);
+                }
+        mx = wave_max(mx);
+        float ex[NV][8];
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = (float)r[k][u][e];
+                ex[u][e] = (lane + 64 * u < nc && v > kMask) ? expf(v * scale - mx) : 0.0f;
+                sum += ex[u][e];
+            }
+        sum = wave_sum(sum);
+        const float inv = 1.0f / fmaxf(sum, 1e-20f);
+        half8* y = reinterpret_cast<half8*>(out + (row0 + k) * D);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int c = lane + 64 * u;
+            if (c >= nc) continue;
+            half8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (f16)(ex[u][e] * inv);
+            y[c] = o;
+        }
     }
 }
 
@@ -451,10 +456,11 @@ __global__ __launch_bounds__(CE_NT) void ce_row_k(const f16* logits, const uint1
 }
 
 // ce_row_k with the row in registers: V % 8 == 0, 16-byte aligned rows,
-// V <= CE_NT * 8 * NV; one HBM read and one write per logit
-template <int NV>
-__global__ __launch_bounds__(CE_NT) void ce_row_reg_k(const f16* logits, const uint16_t* tgt, f16* grad, float* ws,
-                                                      int V) {
+// V <= NT * 8 * NV; one HBM read and one write per logit
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void ce_row_reg_k(const f16* logits, const uint16_t* tgt, f16* grad, float* ws,
+                                                   int V) {
+    constexpr int CE_NT = NT;
     __shared__ float sh[2 * (CE_NT / 64)];
     const int64_t row = blockIdx.x;
     const half8* x = reinterpret_cast<const half8*>(logits + row * V);
@@ -590,12 +596,14 @@ int adam_launch(f16* param, const f16* grad, f16* m, f16* v, int64_t n, float lr
 int softmax_launch(const f16* in, f16* out, float scale, int D, int64_t rows, bool vec, hipStream_t st) {
     if (rows == 0 || D == 0) return EVKHIP_OK;
     if (vec && D % 8 == 0 && D <= 64 * 8 * 4) {
+        const unsigned g2 = (unsigned)((rows + 2 * ROWS_PER_WG - 1) / (2 * ROWS_PER_WG));
         if (D <= 64 * 8)
-            hipLaunchKernelGGL(softmax_reg_k<1>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+            hipLaunchKernelGGL((softmax_reg_k<1, 2>), dim3(g2), dim3(EW_NT), 0, st, in, out, scale, D, rows);
         else if (D <= 64 * 8 * 2)
-            hipLaunchKernelGGL(softmax_reg_k<2>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+            hipLaunchKernelGGL((softmax_reg_k<2, 2>), dim3(g2), dim3(EW_NT), 0, st, in, out, scale, D, rows);
         else
-            hipLaunchKernelGGL(softmax_reg_k<4>, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
+            hipLaunchKernelGGL((softmax_reg_k<4, 1>), dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D,
+                               rows);
         return launched("softmax launch");
     }
     hipLaunchKernelGGL(softmax_k, dim3(row_grid(rows)), dim3(EW_NT), 0, st, in, out, scale, D, rows);
@@ -632,12 +640,13 @@ int cross_entropy_launch(const f16* logits, const uint16_t* tgt, f16* grad, f16*
         g_ce_ws_n = need;
     }
     hipLaunchKernelGGL(ce_count_k, dim3(1), dim3(RED_NT), 0, st, tgt, g_ce_ws, rows, V);
-    if (vec && V % 8 == 0 && V <= CE_NT * 8 * 16) {
+    if (vec && V % 8 == 0 && V <= 512 * 8 * 8) {
         if (V <= CE_NT * 8 * 4)
-            hipLaunchKernelGGL(ce_row_reg_k<4>, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws, V);
+            hipLaunchKernelGGL((ce_row_reg_k<4, CE_NT>), dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad,
+                               g_ce_ws, V);
         else
-            hipLaunchKernelGGL(ce_row_reg_k<16>, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws,
-                               V);
+            hipLaunchKernelGGL((ce_row_reg_k<8, 512>), dim3((unsigned)rows), dim3(512), 0, st, logits, tgt, grad,
+                               g_ce_ws, V);
     } else {
         hipLaunchKernelGGL(ce_row_k, dim3((unsigned)rows), dim3(CE_NT), 0, st, logits, tgt, grad, g_ce_ws, V);
     }
