@@ -464,6 +464,11 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     constexpr int ROWS = L::ROWS;
     constexpr int KS = L::KS, DB = L::DB, VW = L::VW, VPER = L::VPER;
     __shared__ __attribute__((aligned(16))) float smem_all[2 * (L::LDS_BYTES / 4)];
+    __shared__ int half_arrivals[2];  // barrier counters of the two halves
+    if (threadIdx.x == 0) {
+        half_arrivals[0] = 0;
+        half_arrivals[1] = 0;
+    }
 
     // a workgroup runs row tiles nrg-1-q (waves 0-3) and q (waves 4-7) of
     // one batch: under the causal mask every pair carries about the same
@@ -600,20 +605,50 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                         s[kb][qb][j] = (kb * 16 + j > lim) ? -INFINITY : s[kb][qb][j];
             }
         }
-        float mx[QB];
-        bool grow = false;
+        // probabilities against the current references first.  A reference
+        // only moves (rare, a real branch) when its row has none yet or some
+        // probability of the chunk exceeds 2^RESCALE_LOG2; the packed fp16
+        // maximum of the probabilities shows the latter (values past the fp16
+        // range convert to inf), at half the instructions of an fp32 row max
+        half8 pb[QB];
+        auto make_p = [&]() {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            mx[qb] = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
-                           fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
-            grow |= mx[qb] > m_ref[qb] + RESCALE_LOG2;
+            for (int qb = 0; qb < QB; ++qb) {
+                const float nbase = (m_ref[qb] == -INFINITY) ? 0.0f : -m_ref[qb];
+                float e[2][4];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) e[kb][j] = fast_exp2(__builtin_fmaf(s[kb][qb][j], c2, nbase));
+                u32x4 u = {pack_h2(e[0][0], e[0][1]), pack_h2(e[0][2], e[0][3]),
+                           pack_h2(e[1][0], e[1][1]), pack_h2(e[1][2], e[1][3])};
+                pb[qb] = as_half8(u);
+            }
+        };
+        bool need = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) need |= m_ref[qb] == -INFINITY;
+        make_p();
+        {
+            half2_t hm[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hm[i] = half2_t{pb[0][2 * i], pb[0][2 * i + 1]};
+#pragma unroll
+                for (int qb = 1; qb < QB; ++qb)
+                    hm[i] = __builtin_elementwise_max(hm[i], half2_t{pb[qb][2 * i], pb[qb][2 * i + 1]});
+            }
+            const half2_t h = __builtin_elementwise_max(__builtin_elementwise_max(hm[0], hm[1]),
+                                                        __builtin_elementwise_max(hm[2], hm[3]));
+            need |= __builtin_fmaxf((float)h[0], (float)h[1]) > (float)(1 << (int)RESCALE_LOG2);
         }
-        // rare (lazy rescale): a real branch, kept out of the common path
-        if (__builtin_expect(__any(grow), 0)) {
+        if (__builtin_expect(__any(need), 0)) {
             asm volatile("" ::: "memory");
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                float m = fmaxf(mx[qb], __shfl_xor(mx[qb], 16, 64));
+                float m = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
+                                fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
+                m = fmaxf(m, __shfl_xor(m, 16, 64));
                 m = fmaxf(m, __shfl_xor(m, 32, 64));
                 const float m_new = fmaxf(m_ref[qb], m);
                 const float alpha = (m_ref[qb] == -INFINITY) ? 0.0f : fast_exp2(m_ref[qb] - m_new);
@@ -622,21 +657,10 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                 lacc[qb] *= alpha;
                 m_ref[qb] = m_new;
             }
+            make_p();
         }
-        half8 pb[QB];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-            const float nbase = (m_ref[qb] == -INFINITY) ? 0.0f : -m_ref[qb];
-            float e[2][4];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) e[kb][j] = fast_exp2(__builtin_fmaf(s[kb][qb][j], c2, nbase));
-            u32x4 u = {pack_h2(e[0][0], e[0][1]), pack_h2(e[0][2], e[0][3]),
-                       pack_h2(e[1][0], e[1][1]), pack_h2(e[1][2], e[1][3])};
-            pb[qb] = as_half8(u);
-            lacc[qb] = mfma16(ones8, pb[qb], lacc[qb]);
-        }
+        for (int qb = 0; qb < QB; ++qb) lacc[qb] = mfma16(ones8, pb[qb], lacc[qb]);
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
             const f16* base0 = vslot + (g * 4 + trow) * VW + d * 16 + tcol;
@@ -650,14 +674,26 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 
     // ---- merge the four waves' partial softmax states ----
     // Each wave stores its state as it stands (m, l and O relative to its own
-    // running max); after one barrier the lanes that write a row combine the
-    // four with weights 2^(m_w - m).  Merge addresses derive from an opaque
+    // running max); after a barrier of the half's four waves the lanes that
+    // write a row combine the four with weights 2^(m_w - m).  Merge addresses derive from an opaque
     // copy of the lane id, so the compiler computes them here instead of
     // keeping them live through the loop.
     int ml = lane;
     asm volatile("" : "+v"(ml));
     const int ml16 = ml & 15, mg = ml >> 4;
-    __syncthreads();  // every wave is done with its V slot
+    // Barrier of the four waves of this half (a counter in LDS): the halves
+    // finish their loops at different times, and neither waits for the other
+    // to merge.  Every wave of the half arrives; the wait is bounded anyway.
+    auto half_sync = [&](int target) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&half_arrivals[half], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (int it = 0; it < (1 << 22); ++it) {
+            if (__hip_atomic_load(&half_arrivals[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+    half_sync(4);  // every wave of the half is done with its V slot
     float* ob = smem_f;                          // [wave][ROWS][OW]
     float* mw = smem_f + 4 * ROWS * L::OW;       // [wave][ROWS]
     float* lw = mw + 4 * ROWS;                   // [wave][ROWS]
@@ -672,7 +708,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         for (int d = 0; d < DB; ++d)
             *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb];
     }
-    __syncthreads();
+    half_sync(8);
     // wave w finishes rows [w*ROWS/4, (w+1)*ROWS/4): a lane owns 8 dh of one row
     constexpr int CPR = DH / 8, RPW = ROWS / 4;
     for (int rr = ml / CPR; rr < RPW; rr += 64 / CPR) {
