@@ -19,6 +19,12 @@
 #include <math.h>
 
 namespace evkhip {
+
+// e^x as 2^(x log2 e) on v_exp_f32: the row maximum is subtracted inside one
+// FMA, exp(a - m) = 2^(a log2e - m log2e)
+constexpr float kLog2eT = 1.4426950408889634f;
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 namespace {
 
 constexpr int EW_NT = 256;  // threads of an elementwise workgroup
@@ -252,16 +258,17 @@ __global__ __launch_bounds__(EW_NT) void softmax_k(const f16* in, f16* out, floa
         if (r > kMask) mx = fmaxf(mx, r * scale);
     }
     mx = wave_max(mx);
+    const float sl2 = scale * kLog2eT, nm2 = -mx * kLog2eT;
     float sum = 0.0f;
     for (int j = lane; j < D; j += 64) {
         const float r = hf(x[j]);
-        if (r > kMask) sum += expf(r * scale - mx);
+        if (r > kMask) sum += exp2_fast(__builtin_fmaf(r, sl2, nm2));
     }
     sum = wave_sum(sum);
     const float inv = 1.0f / fmaxf(sum, 1e-20f);
     for (int j = lane; j < D; j += 64) {
         const float r = hf(x[j]);
-        y[j] = (f16)(r > kMask ? expf(r * scale - mx) * inv : 0.0f);
+        y[j] = (f16)(r > kMask ? exp2_fast(__builtin_fmaf(r, sl2, nm2)) * inv : 0.0f);
     }
 }
 
@@ -297,6 +304,7 @@ __global__ __launch_bounds__(EW_NT) void softmax_reg_k(const f16* in, f16* out, 
                     if (v > kMask) mx = fmaxf(mx, v * scale);
                 }
         mx = wave_max(mx);
+        const float sl2 = scale * kLog2eT, nm2 = -mx * kLog2eT;
         float ex[NV][8];
         float sum = 0.0f;
 #pragma unroll
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(EW_NT) void softmax_reg_k(const f16* in, f16* out, 
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = (float)r[k][u][e];
-                ex[u][e] = (lane + 64 * u < nc && v > kMask) ? expf(v * scale - mx) : 0.0f;
+                ex[u][e] = (lane + 64 * u < nc && v > kMask) ? exp2_fast(__builtin_fmaf(v, sl2, nm2)) : 0.0f;
                 sum += ex[u][e];
             }
         sum = wave_sum(sum);
@@ -437,8 +445,9 @@ __global__ __launch_bounds__(CE_NT) void ce_row_k(const f16* logits, const uint1
     mx = sh[0];
 #pragma unroll
     for (int w = 1; w < CE_NT / 64; ++w) mx = fmaxf(mx, sh[w]);
+    const float nm2 = -mx * kLog2eT;
     float sum = 0.0f;
-    for (int j = threadIdx.x; j < V; j += CE_NT) sum += expf(lv(j) - mx);
+    for (int j = threadIdx.x; j < V; j += CE_NT) sum += exp2_fast(__builtin_fmaf(lv(j), kLog2eT, nm2));
     sum = wave_sum(sum);
     if ((threadIdx.x & 63) == 0) sh[CE_NT / 64 + (threadIdx.x >> 6)] = sum;
     __syncthreads();
@@ -447,8 +456,9 @@ __global__ __launch_bounds__(CE_NT) void ce_row_k(const f16* logits, const uint1
     for (int w = 0; w < CE_NT / 64; ++w) sum += sh[CE_NT / 64 + w];
     sum = fmaxf(sum, 1e-20f);
     const float inv_sum = 1.0f / sum, log_sum = logf(sum);
+    const float scale_g = inv_sum * inv_valid;
     for (int j = threadIdx.x; j < V; j += CE_NT) {
-        float gv = expf(lv(j) - mx) * inv_sum * inv_valid;
+        float gv = exp2_fast(__builtin_fmaf(lv(j), kLog2eT, nm2)) * scale_g;
         if (j == t) gv -= inv_valid;
         g[j] = (f16)gv;
     }
@@ -494,12 +504,13 @@ __global__ __launch_bounds__(NT) void ce_row_reg_k(const f16* logits, const uint
     mx = sh[0];
 #pragma unroll
     for (int w = 1; w < CE_NT / 64; ++w) mx = fmaxf(mx, sh[w]);
+    const float nm2 = -mx * kLog2eT;
     float sum = 0.0f;
 #pragma unroll
     for (int u = 0; u < NV; ++u)
         if (threadIdx.x + CE_NT * u < nc)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sum += expf(cl(r[u][e]) - mx);
+            for (int e = 0; e < 8; ++e) sum += exp2_fast(__builtin_fmaf(cl(r[u][e]), kLog2eT, nm2));
     sum = wave_sum(sum);
     if ((threadIdx.x & 63) == 0) sh[CE_NT / 64 + (threadIdx.x >> 6)] = sum;
     __syncthreads();
@@ -509,19 +520,22 @@ __global__ __launch_bounds__(NT) void ce_row_reg_k(const f16* logits, const uint
     sum = fmaxf(sum, 1e-20f);
     const float inv_valid = 1.0f / n_valid;
     const float inv_sum = 1.0f / sum, log_sum = logf(sum);
+    const float scale_g = inv_sum * inv_valid;
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int c = threadIdx.x + CE_NT * u;
         if (c >= nc) continue;
         half8 o;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float gv = expf(cl(r[u][e]) - mx) * inv_sum * inv_valid;
-            if (c * 8 + e == t) {
-                gv -= inv_valid;
-                ws[1 + row] = ((mx + log_sum) - cl(r[u][e])) * inv_valid;
-            }
-            o[e] = (f16)gv;
+        for (int e = 0; e < 8; ++e) o[e] = (f16)(exp2_fast(__builtin_fmaf(cl(r[u][e]), kLog2eT, nm2)) * scale_g);
+        if (c == (t >> 3)) {  // the target's chunk: its gradient and the row loss
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (e == (t & 7)) {
+                    const float xv = cl(r[u][e]);
+                    o[e] = (f16)(exp2_fast(__builtin_fmaf(xv, kLog2eT, nm2)) * scale_g - inv_valid);
+                    ws[1 + row] = ((mx + log_sum) - xv) * inv_valid;
+                }
         }
         g[c] = o;
     }
