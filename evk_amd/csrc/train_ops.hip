@@ -138,17 +138,19 @@ struct AdamArgs {
 DEV void adam_one(const AdamArgs& a, float g, float& p, float& mq, float& vq) {
     const float kOffset = 41.0f, kMinRms = 1.0e-12f;
     if (!isfinite(g)) return;
-    float rms = vq > 0.0f ? exp2f(vq - kOffset) : 0.0f;
+    // hardware exp2 / log2 / sqrt / reciprocal (about 1 ulp in fp32): the
+    // state and the parameter are stored in fp16, far coarser than that
+    float rms = vq > 0.0f ? __builtin_amdgcn_exp2f(vq - kOffset) : 0.0f;
     float m = mq * rms;
     float v = rms * rms;
     m = a.beta1 * m + (1.0f - a.beta1) * g;
     v = a.beta2 * v + (1.0f - a.beta2) * g * g;
-    rms = sqrtf(fmaxf(v, 0.0f));
-    const float m_norm = m / fmaxf(rms, 1.0e-8f);
+    rms = __builtin_amdgcn_sqrtf(fmaxf(v, 0.0f));
+    const float m_norm = m * __builtin_amdgcn_rcpf(fmaxf(rms, 1.0e-8f));
     if (isfinite(m_norm)) mq = m_norm;
-    const float log_rms = log2f(fmaxf(rms, kMinRms)) + kOffset;
+    const float log_rms = __builtin_amdgcn_logf(fmaxf(rms, kMinRms)) + kOffset;
     if (isfinite(log_rms)) vq = log_rms;
-    const float upd = a.lr * (m * a.c1inv) / (rms * sqrtf(a.c2inv) + a.eps);
+    const float upd = a.lr * (m * a.c1inv) * __builtin_amdgcn_rcpf(rms * __builtin_amdgcn_sqrtf(a.c2inv) + a.eps);
     if (isfinite(upd)) p = fminf(fmaxf(p - upd, -65504.0f), 65504.0f);
 }
 // 8 elements per thread; a value that is not updated is stored back as it
