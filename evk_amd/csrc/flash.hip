@@ -1039,18 +1039,20 @@ __global__ __launch_bounds__(256) void flash_bwd_kv_reduce(FlashArgs p, const fl
     if (nparts == 1) return;  // written directly by its only part
     for (int e = slice * 256 + threadIdx.x; e < SLOT; e += 16 * 256) {
         const floatx4* src = reinterpret_cast<const floatx4*>(part_ws) + ((int64_t)b * parts_per_batch + slot0) * SLOT + e;
-        // part order as written; loads go out 8 at a time so that their
-        // latencies overlap
-        floatx4 acc = src[0];
-        int q = 1;
-        for (; q + 8 <= nparts; q += 8) {
-            floatx4 v[8];
+        // part order as written; up to 16 loads go out together (predicated,
+        // no serial tail) so that their latencies overlap
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < nparts; q += 16) {
+            floatx4 v[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(q + u) * SLOT];
+            for (int u = 0; u < 16; ++u)
+                if (q + u < nparts) v[u] = src[(int64_t)(q + u) * SLOT];
+            if (q == 0) acc = v[0];
+            else acc += v[0];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc += v[u];
+            for (int u = 1; u < 16; ++u)
+                if (q + u < nparts) acc += v[u];
         }
-        for (; q < nparts; ++q) acc += src[(int64_t)q * SLOT];
         // e = ((wave * 2 + which) * 2 + k2) * DB + d) * 64 + lane
         const int lane = e % 64, d = (e / 64) % DB, k2 = (e / (64 * DB)) % 2, which = (e / (64 * DB * 2)) % 2,
                   wave = e / (64 * PW);
