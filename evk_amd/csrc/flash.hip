@@ -863,6 +863,19 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
     u32x4 pr[PPT], po = {0u, 0u, 0u, 0u};
     float sr = 0.0f;
     int spos = 0;
+    // Row (position, head) of thread t's statistics row (t mod BRC), advanced
+    // by BRC rows per chunk without dividing: gload(c) is called for c_lo,
+    // c_lo + 1, ... in order.
+    const int h_step = BRC % H, p_step = BRC / H;
+    int st_head, st_pos;
+    {
+        const int row = r_lo + c_lo * BRC + (int)(threadIdx.x % BRC);
+        st_head = row % H;
+        st_pos = row / H;
+    }
+    int st_next = c_lo;
+    // The LSE value is kept as loaded (lstore scales it), so that nothing
+    // waits for the load here.
     auto gload = [&](int c) {
         const uint32_t row0 = (uint32_t)(r_lo + c * BRC);
 #pragma unroll
@@ -875,11 +888,19 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
                 if (which) po = buf_load16(ores, off, 0);
             }
         }
-        if (threadIdx.x < BRC) {  // base-2 LSE of row row0 + t, from the (B, H, N) LSE
+        for (; st_next < c; ++st_next) {
+            st_head += h_step;
+            st_pos += p_step;
+            if (st_head >= H) {
+                st_head -= H;
+                st_pos += 1;
+            }
+        }
+        if (threadIdx.x < BRC) {  // LSE of row row0 + t, from the (B, H, N) LSE
             const uint32_t row = row0 + threadIdx.x;
-            sr = row < (uint32_t)NH ? p.lse[((int64_t)b * H + row % H) * N + row / H] * kLog2e : 0.0f;
+            sr = row < (uint32_t)NH ? p.lse[((int64_t)b * H + st_head) * N + st_pos] : 0.0f;
         } else if (threadIdx.x < 2 * BRC) {
-            spos = (int)((row0 + threadIdx.x - BRC) / (uint32_t)H);
+            spos = st_pos;
         }
     };
     auto lstore = [&](int stage) {
@@ -903,7 +924,7 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
             if (pc >= PIECES && pc < 2 * PIECES && pi % (DH / 8) == 0)
                 stats_s[stage * L::STATS + BRC + pi / (DH / 8)] = dsum;
         }
-        if (threadIdx.x < BRC) stats_s[stage * L::STATS + threadIdx.x] = sr;
+        if (threadIdx.x < BRC) stats_s[stage * L::STATS + threadIdx.x] = sr * kLog2e;  // base-2 LSE
         else if (threadIdx.x < 2 * BRC) pos_s[stage * BRC + threadIdx.x - BRC] = spos;
     };
 
@@ -923,6 +944,18 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
             const f16* qs = chunk_s + stage * L::STAGE;
             const f16* gs = qs + L::CHUNK;
             const float* st = stats_s + stage * L::STATS;
+            // row statistics of the chunk, read before the MFMAs so that the
+            // LDS latency hides behind them
+            const int* ps_ = pos_s + stage * BRC;
+            floatx4 l2v[2], ddv[2];
+            intx4 psv[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                l2v[rb] = *reinterpret_cast<const floatx4*>(st + rb * 16 + 4 * g);
+                ddv[rb] = *reinterpret_cast<const floatx4*>(st + BRC + rb * 16 + 4 * g);
+                psv[rb] = *reinterpret_cast<const intx4*>(ps_ + rb * 16 + 4 * g);
+            }
+            const int pos_min = ps_[0];
             floatx4 s[2][2], dp[2][2];  // [row block][key block]
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -946,8 +979,6 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
             // element j of s[rb][k2]: row row0 + 16 rb + 4 g + j, key k0 + 16 k2 + l16
             // masking only where some key of this wave can exceed some row's
             // position (or lie past N)
-            const int* ps_ = pos_s + stage * BRC;
-            const int pos_min = ps_[0];
             const bool edge = (CAUSAL && pos_min < k0 + 31) || k0 + 31 >= N;
             half8 pa[2], da[2];
 #pragma unroll
@@ -956,9 +987,8 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
                 float pv[2][4], dsv[2][4];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb) {
-                    const floatx4 l2 = *reinterpret_cast<const floatx4*>(st + rb * 16 + 4 * g);
-                    const floatx4 dd = *reinterpret_cast<const floatx4*>(st + BRC + rb * 16 + 4 * g);
-                    const intx4 ps = *reinterpret_cast<const intx4*>(ps_ + rb * 16 + 4 * g);
+                    const floatx4 l2 = l2v[rb], dd = ddv[rb];
+                    const intx4 ps = psv[rb];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         float pe = fast_exp2(__builtin_fmaf(s[rb][k2][j], c2, -l2[j]));
