@@ -53,6 +53,26 @@ def test_flash_forward_ragged_heads(dev, orc, Dh, N):
         assert np.abs(lse - wl).max() < 1e-2
 
 
+@pytest.mark.parametrize("order", ["growing", "shrinking"])
+def test_flash_forward_moving_maximum(dev, orc, order):
+    """Scores that rise (or fall) by about 18 (base 2) per 32-key chunk along
+    the keys: with growing scores every chunk moves the running maximum past
+    the lazy-rescale threshold, with shrinking ones most probabilities of a
+    row underflow against its first chunk."""
+    import evk_amd as evk
+    B, H, S, Dh = 1, 8, 1024, 64
+    rng = np.random.default_rng(231)
+    q = f16(1.0 + 0.01 * rng.standard_normal((B, S, H * Dh)))
+    ramp = np.arange(S) * 0.05 if order == "growing" else (S - 1 - np.arange(S)) * 0.05
+    k = f16(ramp[None, :, None] * (1.0 + 0.01 * rng.standard_normal((B, S, Dh))))
+    v = orc.normal_f16((B, S, Dh), 232)
+    for causal in (True, False):
+        o, lse = fwd(evk, dev, q, k, v, causal)
+        wo, wl = orc.attention_fwd(q, k, v, causal)
+        assert_close_f16(o, wo, what=f"O {order} causal={causal}")
+        assert np.abs(lse - wl).max() < 1e-2 * max(1.0, np.abs(wl).max() / 100)
+
+
 def test_flash_forward_row_sums(dev, orc):
     # V == 1 -> every output is exactly the softmax row sum: within 1e-3 of 1
     import evk_amd as evk
