@@ -61,6 +61,9 @@ SIGNATURES = {
     "evkhip_last_error": (C.c_char_p, []),
     "evkhip_init": (C.c_int, []),
     "evkhip_shutdown": (C.c_int, []),
+    "evkhip_device_status": (C.c_int, [C.POINTER(C.c_uint32), C.c_int]),
+    "evkhip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
+    "evkhip_flash_has_mfma": (C.c_int, [C.c_uint32]),
     "evkhip_matmul": (C.c_int, [TP, TP, TP, C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_uint32,
                                 C.c_void_p]),
     "evkhip_flash_attention": (C.c_int, [TP, TP, TP, TP, C.c_int, C.c_void_p, C.c_void_p]),
@@ -74,6 +77,7 @@ SIGNATURES = {
     "evkhip_add": (C.c_int, [TP, TP, TP, C.c_void_p]),
     "evkhip_embed": (C.c_int, [TP, TP, TP, C.c_void_p]),
     "evkhip_greedy_sample": (C.c_int, [TP, TP, C.c_uint32, C.c_uint16, C.c_uint16, C.c_void_p]),
+    "evkhip_fill": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p]),
     "evkhip_scale": (C.c_int, [TP, C.c_float, C.c_void_p]),
     "evkhip_relu": (C.c_int, [TP, TP, C.c_void_p]),
     "evkhip_relu_backward": (C.c_int, [TP, TP, TP, C.c_void_p]),
@@ -170,6 +174,21 @@ def initialize() -> None:
 def shutdown() -> None:
     """evk::ai::shutdown (evk_ai.cpp:248-252): frees library workspace."""
     _check(lib().evkhip_shutdown())
+
+
+STATUS_WAIT_TIMEOUT = 1
+
+
+def device_status(clear=False) -> int:
+    """Device status bits (STATUS_*) raised by the kernels; synchronise first."""
+    v = C.c_uint32(0)
+    _check(lib().evkhip_device_status(C.byref(v), int(bool(clear))))
+    return v.value
+
+
+def debug_set_spin_limit(iterations: int) -> None:
+    """Test hook: iterations of the bounded in-kernel waits (0 = default)."""
+    _check(lib().evkhip_debug_set_spin_limit(int(iterations)))
 
 
 def matmul(a, b, c, transpose_a=False, transpose_b=False, acc_c=False, TILE_M=80, TILE_N=80,

@@ -95,6 +95,16 @@ int evkhip_shutdown(void) {
     return EVKHIP_OK;
 }
 
+int evkhip_device_status(uint32_t* flags, int clear) {
+    EVK_RETURN_IF(!flags, EVKHIP_ERR_INVALID_ARG, "device_status: null flags");
+    return flash_status(flags, clear != 0);
+}
+
+int evkhip_debug_set_spin_limit(uint32_t iterations) {
+    flash_set_spin_limit(iterations);
+    return EVKHIP_OK;
+}
+
 int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
                   int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream) {
     CHECK(check_tensor(a, "matmul: a", 2, EVKHIP_MAX_DIMS));
@@ -162,6 +172,8 @@ static int flash_shapes(const evkhip_tensor* q, const evkhip_tensor* k, const ev
     return EVKHIP_OK;
 }
 
+int evkhip_flash_has_mfma(uint32_t head_dim) { return flash_mfma_head(head_dim) ? 1 : 0; }
+
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
                            const evkhip_tensor* o, int causal, float* lse, void* stream) {
     uint32_t B, N, D, Dh;
@@ -169,7 +181,7 @@ int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const
     CHECK(check_tensor(o, "flash_attention: o", 3, 3));
     EVK_RETURN_IF(!same_shape(q, o), EVKHIP_ERR_SHAPE, "flash_attention: o must match q");
     if (B == 0 || N == 0) return EVKHIP_OK;
-    const bool mfma = (Dh == 32 || Dh == 64 || Dh == 128) && aligned16(q->data) && aligned16(k->data) &&
+    const bool mfma = flash_mfma_head(Dh) && aligned16(q->data) && aligned16(k->data) &&
                       aligned16(v->data) && aligned16(o->data);
     FlashArgs a{};
     a.q = (const f16*)q->data;
@@ -205,7 +217,7 @@ int evkhip_flash_attention_bwd(const evkhip_tensor* q, const evkhip_tensor* k, c
         EVK_RETURN_IF(!same_shape(q, o), EVKHIP_ERR_SHAPE, "flash_attention_bwd: o must match q");
     }
     if (B == 0 || N == 0) return EVKHIP_OK;
-    bool mfma = (Dh == 32 || Dh == 64 || Dh == 128);
+    bool mfma = flash_mfma_head(Dh);
     for (const evkhip_tensor* t : {q, k, v, dO, dQ, dK, dV}) mfma = mfma && aligned16(t->data);
     if (lse) mfma = mfma && aligned16(o->data);
     FlashArgs a{};
@@ -323,6 +335,14 @@ static bool all_aligned(std::initializer_list<const evkhip_tensor*> ts) {
     for (const evkhip_tensor* x : ts)
         if (!aligned16(x->data)) return false;
     return true;
+}
+
+int evkhip_fill(void* data, uint64_t bytes, uint32_t pattern, void* stream) {
+    EVK_RETURN_IF(bytes & 1, EVKHIP_ERR_INVALID_ARG, "fill: %llu bytes is not a whole number of 16-bit words",
+                  (unsigned long long)bytes);
+    EVK_RETURN_IF(bytes && (!data || (reinterpret_cast<uintptr_t>(data) & 1)), EVKHIP_ERR_INVALID_ARG,
+                  "fill: null or odd data pointer");
+    return fill_launch(data, pattern, (int64_t)(bytes / 2), aligned16(data), as_stream(stream));
 }
 
 int evkhip_scale(const evkhip_tensor* t, float factor, void* stream) {

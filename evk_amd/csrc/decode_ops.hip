@@ -340,15 +340,20 @@ int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, in
         size_t need = (size_t)heads * nsplit * (2 + dh);
         if (need > g_sq_part_elems) {
             if (g_sq_part) EVK_HIP(hipFree(g_sq_part));
+            // a failed allocation below leaves an empty workspace, never a
+            // stale size over a null pointer
             g_sq_part = nullptr;
+            g_sq_part_elems = 0;
             EVK_HIP(hipMalloc(&g_sq_part, need * sizeof(float)));
             g_sq_part_elems = need;
         }
         if ((size_t)heads > g_sq_cnt_n) {
             if (g_sq_cnt) EVK_HIP(hipFree(g_sq_cnt));
             g_sq_cnt = nullptr;
+            g_sq_cnt_n = 0;
             EVK_HIP(hipMalloc(&g_sq_cnt, heads * sizeof(unsigned)));
-            EVK_HIP(hipMemset(g_sq_cnt, 0, heads * sizeof(unsigned)));
+            // ordered on the launch stream before the first sq_attention
+            EVK_HIP(hipMemsetAsync(g_sq_cnt, 0, heads * sizeof(unsigned), st));
             g_sq_cnt_n = heads;
         }
     }

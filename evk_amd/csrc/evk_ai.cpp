@@ -87,6 +87,8 @@ void matmul(Tensor& a, Tensor& b, Tensor& c, bool transpose_a, bool transpose_b,
     check(evkhip_matmul(&A, &B, &C, transpose_a, transpose_b, acc_c, TILE_M, TILE_N, stream()), "matmul");
 }
 
+bool flash_has_mfma(uint32_t head_dim) { return evkhip_flash_has_mfma(head_dim) != 0; }
+
 void flash_attention(Tensor& q, Tensor& k, Tensor& v, Tensor& o, bool causal, Tensor* lse) {
     evkhip_tensor Q = desc(q), K = desc(k), V = desc(v), O = desc(o);
     float* L = lse_ptr(lse, q, k, "flash_attention");
@@ -145,11 +147,7 @@ void rms_norm(Tensor& input, Tensor& output, float eps) {
 void zero(Tensor& tensor) {
     const uint64_t bytes = uint64_t(tensor.shape.count()) * sizeof(float16_t);
     if (bytes == 0) return;
-    const hipError_t e = hipMemsetAsync(tensor.device_ptr(), 0, bytes, static_cast<hipStream_t>(stream()));
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "evk::ai::zero failed: %s\n", hipGetErrorString(e));
-        std::abort();
-    }
+    check(evkhip_fill(tensor.device_ptr(), bytes, 0u, stream()), "zero");
 }
 
 // ---- training ops (evk_ai.cpp:475-566,593-780,839-943,968-1043,1072-1093) ----

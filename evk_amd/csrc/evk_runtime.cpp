@@ -6,6 +6,7 @@
 // One HIP stream carries every command in issue order; a submission is an
 // event on that stream.
 #include <evk.h>
+#include <evkhip.h>
 
 #include <hip/hip_runtime_api.h>
 
@@ -336,8 +337,9 @@ void Cmd::barrier() {}
 void Cmd::fill(Buffer dst, uint32_t data, uint64_t size, uint64_t offset) {
     BufferRes* b = res_of(dst);
     if (offset + size > b->size || (size & 3) || (offset & 3)) misuse("Cmd::fill: range must be 4-byte aligned and inside the buffer");
-    EVK_CHECK(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(static_cast<char*>(b->dev) + offset), int(data),
-                                size / 4, rt().stream));
+    // a fill kernel, not a memset: a captured graph then holds no memset node
+    if (evkhip_fill(static_cast<char*>(b->dev) + offset, size, data, rt().stream) != 0)
+        misuse(evkhip_last_error());
 }
 
 void Cmd::copy(Buffer& src, Buffer& dst, uint64_t size, uint64_t srcOffset, uint64_t dstOffset) {

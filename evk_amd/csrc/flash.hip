@@ -22,14 +22,21 @@
 // Softmax runs in the exp2 domain: s2 = s * scale * log2(e).
 #include "kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 #include <math.h>
 
 namespace evkhip {
 
+// Status bits raised by the kernels of this file (EVKHIP_STATUS_*).
+__device__ unsigned g_flash_status;
 
 namespace {
+
+// Default iterations (of s_sleep 1) of a bounded in-kernel wait.
+constexpr int kDefaultSpinLimit = 1 << 22;
+int g_spin_limit = kDefaultSpinLimit;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -683,14 +690,22 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     const int ml16 = ml & 15, mg = ml >> 4;
     // Barrier of the four waves of this half (a counter in LDS): the halves
     // finish their loops at different times, and neither waits for the other
-    // to merge.  Every wave of the half arrives; the wait is bounded anyway.
+    // to merge.  Every wave of the half arrives (the four waves of a
+    // workgroup are resident together), but the wait is bounded anyway: a
+    // wave that gives up raises EVKHIP_STATUS_WAIT_TIMEOUT in the device
+    // status word, which the host reads with evkhip_device_status.
     auto half_sync = [&](int target) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) __hip_atomic_fetch_add(&half_arrivals[half], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        for (int it = 0; it < (1 << 22); ++it) {
-            if (__hip_atomic_load(&half_arrivals[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        bool met = false;
+        for (int it = 0;; ++it) {
+            met = __hip_atomic_load(&half_arrivals[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target;
+            if (met || it >= p.spin_limit) break;
             __builtin_amdgcn_s_sleep(1);
         }
+        if (!met && lane == 0)
+            __hip_atomic_fetch_or(&g_flash_status, (unsigned)EVKHIP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
     half_sync(4);  // every wave of the half is done with its V slot
@@ -1771,6 +1786,21 @@ hipError_t launch_bwd_split(const FlashArgs& a, bool causal, float* parts, int p
 
 }  // namespace
 
+int flash_status(uint32_t* flags, bool clear) {
+    unsigned v = 0;
+    EVK_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_flash_status), sizeof(v), 0, hipMemcpyDeviceToHost));
+    if (clear && v) {
+        const unsigned zero = 0;
+        EVK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_flash_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice));
+    }
+    *flags = v;
+    return EVKHIP_OK;
+}
+
+void flash_set_spin_limit(uint32_t n) {
+    g_spin_limit = n == 0 ? kDefaultSpinLimit : (int)std::min<uint32_t>(n - 1, (uint32_t)INT32_MAX);
+}
+
 void flash_free_workspace() {
     if (g_bwd_ws) (void)hipFree(g_bwd_ws);
     g_bwd_ws = nullptr;
@@ -1778,6 +1808,7 @@ void flash_free_workspace() {
 }
 
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
+    a.spin_limit = g_spin_limit;
     a.scale = 1.0f / sqrtf((float)dh);
     a.scale_log2 = a.scale * kLog2e;
     hipError_t e;
@@ -1793,6 +1824,7 @@ int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
 }
 
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
+    a.spin_limit = g_spin_limit;
     a.scale = 1.0f / sqrtf((float)dh);
     a.scale_log2 = a.scale * kLog2e;
     const size_t rows = (size_t)a.B * a.N * a.H;

@@ -33,10 +33,18 @@ struct FlashArgs {
     int B, H, N;
     float scale_log2;  // scale * log2(e)
     float scale;
+    int spin_limit;    // iterations of a bounded in-kernel wait before it gives up
 };
+// Head sizes with MFMA forward and backward kernels.
+inline bool flash_mfma_head(uint32_t dh) { return dh == 32 || dh == 64 || dh == 128; }
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 void flash_free_workspace();
+// Device status bits raised by the flash kernels (EVKHIP_STATUS_*): read after
+// the work has completed; `clear` resets them.
+int flash_status(uint32_t* flags, bool clear);
+// Spin limit of the bounded in-kernel waits (0 restores the default).
+void flash_set_spin_limit(uint32_t n);
 
 // ---- decode_ops.hip ----
 int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, int64_t row_stride, int heads,
@@ -52,6 +60,7 @@ int greedy_launch(const f16* logits, uint16_t* out, int B, int S, int V, int pos
 void decode_ops_free_workspace();
 
 // ---- train_ops.hip (vec: the caller's pointers are 16-byte aligned) ----
+int fill_launch(void* p, uint32_t pattern, int64_t n16, bool vec, hipStream_t st);
 int scale_launch(f16* x, float s, int64_t n, bool vec, hipStream_t st);
 int relu_launch(const f16* in, f16* out, int64_t n, bool vec, hipStream_t st);
 int relu_bwd_launch(const f16* gout, const f16* in, f16* gin, int64_t n, bool vec, hipStream_t st);

@@ -56,6 +56,19 @@ DEV void st8(f16* p, int64_t i0, int64_t n, bool vec, const float (&v)[8]) {
 }
 DEV int64_t first8() { return ((int64_t)blockIdx.x * EW_NT + threadIdx.x) * 8; }
 
+// Fill of `n` 16-bit words with a repeated 32-bit pattern: word i takes the
+// pattern's low half for even i and its high half for odd i.  A kernel, not
+// hipMemsetAsync, so that a captured HIP graph holds no memset node.
+__global__ __launch_bounds__(EW_NT) void fill_k(uint16_t* p, uint32_t pattern, int64_t n, bool vec) {
+    const int64_t i0 = first8();
+    if (i0 >= n) return;
+    if (vec && i0 + 8 <= n) {
+        *reinterpret_cast<u32x4*>(p + i0) = u32x4{pattern, pattern, pattern, pattern};
+    } else {
+        for (int64_t i = i0; i < n && i < i0 + 8; ++i) p[i] = (uint16_t)((i & 1) ? pattern >> 16 : pattern);
+    }
+}
+
 // scale.comp: x = fp16(x * s)
 __global__ __launch_bounds__(EW_NT) void scale_k(f16* x, float s, int64_t n, bool vec) {
     const int64_t i0 = first8();
@@ -575,6 +588,13 @@ void train_ops_free_workspace() {
     if (g_ce_ws) (void)hipFree(g_ce_ws);
     g_ce_ws = nullptr;
     g_ce_ws_n = 0;
+}
+
+int fill_launch(void* p, uint32_t pattern, int64_t n16, bool vec, hipStream_t st) {
+    if (n16 == 0) return EVKHIP_OK;
+    hipLaunchKernelGGL(fill_k, dim3(ew_grid8(n16)), dim3(EW_NT), 0, st, static_cast<uint16_t*>(p), pattern, n16,
+                       vec);
+    return launched("fill launch");
 }
 
 int scale_launch(f16* x, float s, int64_t n, bool vec, hipStream_t st) {

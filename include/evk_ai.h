@@ -347,6 +347,9 @@ void matmul(Tensor& a, Tensor& b, Tensor& c, bool transpose_a = false, bool tran
 // log-sum-exp of each (b, h, i) row: B*H*N fp32 values, so its fp16 element
 // count must be 2*B*H*N (e.g. shape (B, H, N, 2)).
 void flash_attention(Tensor& q, Tensor& k, Tensor& v, Tensor& o, bool causal = false, Tensor* lse = nullptr);
+// Whether the flash kernels for this head size run on the matrix cores (no
+// reference counterpart: the reference's shader has one code path).
+bool flash_has_mfma(uint32_t head_dim);
 
 // Backward (evk_ai.h:503): dQ (B,N,D); dK, dV (B,N,Dh) summed over heads.
 // heads != 0 must equal D/Dh.  With lse from the forward pass the row
@@ -667,6 +670,9 @@ struct Graph {
         const uint32_t B = q.shape[0], N = q.shape[1], D = q.shape[2];
         const float default_scale = 1.0f / std::sqrt(float(D));
         if (scale > 0.0f && scale != default_scale) return causal_attention_unfused(q, k, v, scale);
+        // the fused route needs a head size with MFMA flash kernels; other
+        // sizes keep the reference's matmul + mask + softmax chain (on MFMA)
+        if (!evk::ai::flash_has_mfma(D)) return causal_attention_unfused(q, k, v, scale);
         Tensor& lse = node(Shape({B, 1, N, 2}));  // fp32 log-sum-exp per row
         Tensor& dq = node(q.shape);
         Tensor& dk = node(k.shape);

@@ -60,6 +60,20 @@ int evkhip_init(void);
  * (the grow-only flash scratch, cf. evk_ai.cpp:135-157). */
 int evkhip_shutdown(void);
 
+/* Device status bits.  No counterpart in the reference, whose shaders hold
+ * no in-kernel waits: a kernel of this library that waits for other waves
+ * bounds the wait, and a wave that gives up (the result of that launch is
+ * then unreliable) raises EVKHIP_STATUS_WAIT_TIMEOUT here instead of hanging.
+ * Read after the work has completed (synchronise its stream first); `clear`
+ * resets the bits. */
+#define EVKHIP_STATUS_WAIT_TIMEOUT 1u
+int evkhip_device_status(uint32_t* flags, int clear);
+
+/* Test hook (no reference counterpart): iterations of the bounded in-kernel
+ * waits before they give up; 0 restores the default (2^22).  Lets a test
+ * force the timeout path from the host without any wave actually stalling. */
+int evkhip_debug_set_spin_limit(uint32_t iterations);
+
 /* evk::ai::matmul (evk_ai.h:495, evk_ai.cpp:254-330).
  * C[b] (+)= op(A[b]) . op(B[b]):  A (...,M,K) or (...,K,M) if transpose_a;
  * B (...,K,N) or (...,N,K) if transpose_b; C (...,M,N).  batch = max of the
@@ -80,6 +94,10 @@ int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_t
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k,
                            const evkhip_tensor* v, const evkhip_tensor* o,
                            int causal, float* lse, void* stream);
+
+/* Non-zero when the flash forward and backward run MFMA kernels for this
+ * head size (no reference counterpart); other sizes take a scalar path. */
+int evkhip_flash_has_mfma(uint32_t head_dim);
 
 /* evk::ai::flash_attention_bwd (evk_ai.h:503, evk_ai.cpp:371-473).
  * dQ (B,N,D); dK,dV (B,N,Dh) summed over the H heads sharing them.
@@ -138,6 +156,13 @@ int evkhip_greedy_sample(const evkhip_tensor* logits, const evkhip_tensor* out_t
  * into (grad_in += ...) are accumulated here too; every stored value is
  * rounded to fp16 as the shader rounds it.
  * ------------------------------------------------------------------------- */
+
+/* Device fill by a kernel (so a captured HIP graph holds no memset node):
+ * `bytes` (even) at `data` take the 32-bit little-endian `pattern` repeated;
+ * a trailing 16-bit word takes its low half.  Backs evk::ai::zero
+ * (evk_ai.cpp:139-147, which records vkCmdFillBuffer) and evk::Cmd::fill
+ * (evk.h Cmd::fill, evk_vulkan.cpp vkCmdFillBuffer). */
+int evkhip_fill(void* data, uint64_t bytes, uint32_t pattern, void* stream);
 
 /* evk::ai::scale (evk_ai.h:599, evk_ai.cpp:992-1007, scale.comp): in place,
  * t = t * factor. */

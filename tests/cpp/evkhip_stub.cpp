@@ -78,6 +78,20 @@ int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_t
                   uint32_t tm, uint32_t tn, void* stream) {
     return record("matmul", {a, b, c}, {ta, tb, acc, tm, tn}, {}, stream);
 }
+// The fill really fills (the mock's device memory is host memory), so the
+// evk core's Cmd::fill and evk::ai::zero can be checked by reading back.
+int evkhip_fill(void* data, uint64_t bytes, uint32_t pattern, void* stream) {
+    const int rc = record("fill", {}, {(long long)bytes, (long long)pattern}, {}, stream, data);
+    if (rc) return rc;
+    if (bytes & 1) return EVKHIP_ERR_INVALID_ARG;
+    if (bytes && !mock_stream_access(data, bytes)) return EVKHIP_ERR_INVALID_ARG;
+    uint16_t* p = static_cast<uint16_t*>(data);
+    for (uint64_t i = 0; i < bytes / 2; ++i) p[i] = uint16_t((i & 1) ? pattern >> 16 : pattern);
+    return EVKHIP_OK;
+}
+int evkhip_flash_has_mfma(uint32_t head_dim) {
+    return head_dim == 32 || head_dim == 64 || head_dim == 128;
+}
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
                            const evkhip_tensor* o, int causal, float* lse, void* stream) {
     return record("flash_attention", {q, k, v, o}, {causal}, {}, stream, lse);

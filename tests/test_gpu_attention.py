@@ -228,3 +228,58 @@ def test_sq_attention_matches_causal_flash_row(dev, orc):
     o, _ = fwd(evk, dev, q, k, v, True)
     got = sq(evk, dev, q[0, N - 1], k[0], v[0], N, 1)
     assert np.abs(f32(got) - f32(o[0, N - 1])).max() <= 2e-3
+
+
+def test_flash_forward_wait_timeout_is_reported(dev, orc):
+    """The key-split forward's in-kernel wait is bounded: forced from the host
+    to give up at once (spin limit 1, i.e. no sleep), the kernel still exits
+    and raises STATUS_WAIT_TIMEOUT; with the default limit a rerun is clean
+    and matches the oracle.  No wave stalls in either run."""
+    import torch
+    import evk_amd as evk
+    B, H, S, Dh = 4, 8, 1024, 64
+    q = orc.normal_f16((B, S, H * Dh), 201)
+    k = orc.normal_f16((B, S, Dh), 202)
+    v = orc.normal_f16((B, S, Dh), 203)
+    torch.cuda.synchronize()
+    evk.device_status(clear=True)
+    try:
+        evk.debug_set_spin_limit(1)
+        for _ in range(4):
+            fwd(evk, dev, q, k, v, True)
+        torch.cuda.synchronize()
+        forced = evk.device_status(clear=True)
+    finally:
+        evk.debug_set_spin_limit(0)
+    assert forced & evk.STATUS_WAIT_TIMEOUT
+    o, _ = fwd(evk, dev, q, k, v, True)
+    torch.cuda.synchronize()
+    assert evk.device_status(clear=True) == 0
+    wo, _ = orc.attention_fwd(q, k, v, True)
+    assert_close_f16(o, wo, what="O after the forced timeouts")
+
+
+def test_flash_forward_nan_input_propagates(dev, orc):
+    """A NaN in one query row makes that row's output NaN (as the reference's
+    arithmetic would) and leaves every other row as the oracle has it: the
+    kernels make no no-NaN assumption."""
+    import evk_amd as evk
+    B, H, S, Dh = 1, 2, 256, 64
+    q = orc.normal_f16((B, S, H * Dh), 231)
+    k = orc.normal_f16((B, S, Dh), 232)
+    v = orc.normal_f16((B, S, Dh), 233)
+    pos, h = 100, 1
+    q[0, pos, h * Dh + 5] = 0x7E00  # fp16 quiet NaN
+    for causal in (True, False):
+        o, _ = fwd(evk, dev, q, k, v, causal)
+        g = f32(o).reshape(B, S, H, Dh)
+        assert np.isnan(g[0, pos, h]).all(), "NaN query row must give a NaN output row"
+        qc = q.copy()
+        qc[0, pos, h * Dh + 5] = 0
+        wo, _ = orc.attention_fwd(qc, k, v, causal)
+        w = f32(wo).reshape(B, S, H, Dh)
+        mask = np.ones((S, H), bool)
+        mask[pos, h] = False
+        got, want = g[0][mask], w[0][mask]
+        assert np.all(np.isfinite(got))
+        assert np.abs(got - want).max() <= 1e-2 + 1e-2 * np.abs(want).max()

@@ -177,3 +177,35 @@ def test_config5_qkv_shape(dev, orc):
     err = np.abs(G.astype(np.float64).sum(0) - A.sum(0) @ B)
     bound = half_ulp(G).sum(0) + 1e-2 * np.sqrt(M)
     assert np.all(err <= bound), float((err - bound).max())
+
+
+@pytest.mark.parametrize("ta", [False, True])
+def test_operand_over_2gib_takes_tiled_path(dev, orc, ta):
+    """A 2.15 GB A operand (past the 32-bit buffer-descriptor range of the
+    MFMA kernel) runs the 64-bit-addressed tiled kernel; sampled rows of C and
+    whole-matrix column sums are checked against fp32 on the host.  Inputs
+    are drawn on the device from a seeded torch generator (2 GB is too much
+    to push from the host in a test)."""
+    import torch
+    import evk_amd as evk
+    M, K, N = 131072 + 64, 8192, 256
+    assert M * K * 2 > 2**31
+    g = torch.Generator(device=dev).manual_seed(7)
+    shape_a = (K, M) if ta else (M, K)
+    A = (torch.rand(shape_a, generator=g, device=dev, dtype=torch.float16) * 2 - 1)
+    B = (torch.rand((K, N), generator=g, device=dev, dtype=torch.float16) * 2 - 1)
+    C = torch.empty((M, N), dtype=torch.float16, device=dev)
+    evk.matmul(A, B, C, ta, False, False)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 255, 256, 70000, M // 2 + 3, M - 65, M - 1], device=dev)
+    a_rows = (A[:, rows].t() if ta else A[rows]).float().cpu().numpy()
+    want = a_rows @ B.float().cpu().numpy()
+    got = C[rows].float().cpu().numpy()
+    assert np.abs(got - want).max() <= 1e-2 * (1 + np.abs(want).max())
+    # every row: column sums of C against (column sums of A) . B
+    a_sum = (A.float().sum(dim=1) if ta else A.float().sum(dim=0)).cpu().numpy()
+    want_cs = a_sum @ B.float().cpu().numpy()
+    got_cs = C.float().sum(dim=0).cpu().numpy()
+    assert np.abs(got_cs - want_cs).max() <= 2e-3 * np.abs(want_cs).max() + 1.0
+    del A, B, C
+    torch.cuda.empty_cache()
