@@ -66,6 +66,8 @@ SIGNATURES = {
     "evkhip_flash_has_mfma": (C.c_int, [C.c_uint32]),
     "evkhip_matmul": (C.c_int, [TP, TP, TP, C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_uint32,
                                 C.c_void_p]),
+    "evkhip_matmul_noalloc": (C.c_int, [TP, TP, TP, C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_uint32,
+                                        C.c_void_p]),
     "evkhip_flash_attention": (C.c_int, [TP, TP, TP, TP, C.c_int, C.c_void_p, C.c_void_p]),
     "evkhip_flash_attention_bwd": (C.c_int, [TP, TP, TP, TP, TP, TP, TP, TP, C.c_uint32, C.c_int,
                                              C.c_void_p, C.c_void_p]),

@@ -83,7 +83,8 @@ int evkhip_init(void) {
     int dev = 0;
     EVK_HIP(hipGetDevice(&dev));
     (void)device_cu_count();
-    return EVKHIP_OK;
+    GemvScratch s{};
+    return noalloc_scratch(&s);  // the static scratch's address on this device
 }
 
 int evkhip_shutdown(void) {
@@ -105,8 +106,9 @@ int evkhip_debug_set_spin_limit(uint32_t iterations) {
     return EVKHIP_OK;
 }
 
-int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
-                  int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream) {
+static int matmul_impl(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
+                       int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream,
+                       const GemvScratch* fixed) {
     CHECK(check_tensor(a, "matmul: a", 2, EVKHIP_MAX_DIMS));
     CHECK(check_tensor(b, "matmul: b", 2, EVKHIP_MAX_DIMS));
     CHECK(check_tensor(c, "matmul: c", 2, EVKHIP_MAX_DIMS));
@@ -148,10 +150,21 @@ int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_t
     if (K == 0) {
         // C = 0 (or unchanged with acc): a GEMM with an empty contraction
         if (acc_c) return EVKHIP_OK;
-        EVK_HIP(hipMemsetAsync(c->data, 0, numel(c) * 2, as_stream(stream)));
-        return EVKHIP_OK;
+        return fill_launch(c->data, 0u, (int64_t)numel(c), aligned16(c->data), as_stream(stream));
     }
-    return gemm_dispatch(g, (int)batch, transpose_a != 0, transpose_b != 0, vec_ok, as_stream(stream));
+    return gemm_dispatch(g, (int)batch, transpose_a != 0, transpose_b != 0, vec_ok, as_stream(stream), fixed);
+}
+
+int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
+                  int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream) {
+    return matmul_impl(a, b, c, transpose_a, transpose_b, acc_c, tile_m, tile_n, stream, nullptr);
+}
+
+int evkhip_matmul_noalloc(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c, int transpose_a,
+                          int transpose_b, int acc_c, uint32_t tile_m, uint32_t tile_n, void* stream) {
+    GemvScratch s{};
+    CHECK(noalloc_scratch(&s));
+    return matmul_impl(a, b, c, transpose_a, transpose_b, acc_c, tile_m, tile_n, stream, &s);
 }
 
 static int flash_shapes(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,

@@ -773,7 +773,37 @@ static int gemv_workspace(size_t part_elems, size_t n_counters, hipStream_t st) 
 // Picks a kernel for one evk::ai::matmul call.  Shapes were validated by the
 // caller; `vec_ok` says every operand is 16-byte aligned with row lengths
 // that are multiples of 8 halves.
-int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, hipStream_t st) {
+// ---- static scratch of evkhip_matmul_noalloc ----
+// Device memory of the library itself, for callers that cannot allocate:
+// arrival counters, then fp32 split-K partials.  Each GPU holds its own copy
+// at its own address (hipGetSymbolAddress, once per device); host code uses
+// only that address, never the symbol itself.
+constexpr size_t kScratchCounterBytes = 64u << 10;
+constexpr size_t kScratchBytes = kScratchCounterBytes + EVKHIP_NOALLOC_PART_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_addr[kMaxDevices] = {};
+
+int noalloc_scratch(GemvScratch* out) {
+    int dev = 0;
+    EVK_HIP(hipGetDevice(&dev));
+    EVK_RETURN_IF(dev < 0 || dev >= kMaxDevices, EVKHIP_ERR_UNSUPPORTED, "noalloc scratch: device %d", dev);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        EVK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        EVK_RETURN_IF(!p, EVKHIP_ERR_HIP, "noalloc scratch: no device address");
+        g_scratch_addr[dev] = p;
+    }
+    char* base = static_cast<char*>(g_scratch_addr[dev]);
+    out->counters = reinterpret_cast<unsigned*>(base);
+    out->n_counters = kScratchCounterBytes / sizeof(unsigned);
+    out->part = reinterpret_cast<float*>(base + kScratchCounterBytes);
+    out->part_elems = EVKHIP_NOALLOC_PART_BYTES / sizeof(float);
+    return EVKHIP_OK;
+}
+
+int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, hipStream_t st,
+                  const GemvScratch* fixed) {
     if (a.M == 0 || a.N == 0) return EVKHIP_OK;
     hipError_t e;
     if (!vec_ok) {
@@ -789,10 +819,26 @@ int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, h
         float* part = nullptr;
         unsigned* cnt = nullptr;
         if (nks > 1) {
-            int rc = gemv_workspace((size_t)batch * nks * a.M * a.N, (size_t)batch * ncb, st);
-            if (rc) return rc;
-            part = g_gemv_ws.part;
-            cnt = g_gemv_ws.counters;
+            const size_t need_part = (size_t)batch * nks * a.M * a.N, need_cnt = (size_t)batch * ncb;
+            if (fixed) {
+                EVK_RETURN_IF(need_part > fixed->part_elems || need_cnt > fixed->n_counters,
+                              EVKHIP_ERR_UNSUPPORTED,
+                              "matmul_noalloc: the split-K pass needs %zu partial bytes and %zu counters; the "
+                              "static scratch holds %zu and %zu",
+                              need_part * sizeof(float), need_cnt, fixed->part_elems * sizeof(float),
+                              fixed->n_counters);
+                part = fixed->part;
+                cnt = fixed->counters;
+                // the counters start at zero (a fill kernel: no memset node
+                // under graph capture)
+                int rc = fill_launch(cnt, 0u, (int64_t)(need_cnt * 2), true, st);
+                if (rc) return rc;
+            } else {
+                int rc = gemv_workspace(need_part, need_cnt, st);
+                if (rc) return rc;
+                part = g_gemv_ws.part;
+                cnt = g_gemv_ws.counters;
+            }
         }
         dim3 grid(ncb, nks, batch);
         if (a.M <= 1) hipLaunchKernelGGL(gemv_sk<1>, grid, dim3(256), 0, st, a, part, cnt);

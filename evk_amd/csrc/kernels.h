@@ -14,7 +14,19 @@ struct GemmArgs {
     int64_t sA, sB, sC;  // per-batch element strides (0 = broadcast)
     int acc;
 };
-int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, hipStream_t st);
+// Caller-provided split-K scratch of the skinny (M <= 16) path: partials and
+// arrival counters.  With it, gemm_dispatch allocates nothing.
+struct GemvScratch {
+    float* part;
+    size_t part_elems;
+    unsigned* counters;
+    size_t n_counters;
+};
+int gemm_dispatch(const GemmArgs& a, int batch, bool ta, bool tb, bool vec_ok, hipStream_t st,
+                  const GemvScratch* fixed = nullptr);
+// The static per-device scratch of evkhip_matmul_noalloc, for the current
+// device (its address is looked up once per device).
+int noalloc_scratch(GemvScratch* out);
 void gemm_free_workspace();
 
 // ---- flash.hip ----

@@ -86,6 +86,22 @@ int evkhip_matmul(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_t
                   int transpose_a, int transpose_b, int acc_c,
                   uint32_t tile_m, uint32_t tile_n, void* stream);
 
+/* evk::ai::matmul for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference.  Same arguments, results, errors and
+ * kernels as evkhip_matmul, but it never allocates: the split-K partials and
+ * arrival counters of the skinny (M <= 16) path live in a static per-device
+ * array of EVKHIP_NOALLOC_PART_BYTES of partials (plus 64 KiB of counters),
+ * held by each GPU the library runs on until the process ends.  A call whose
+ * split-K pass needs more (batch * ceil(K/512) * M * N * 4 bytes) returns
+ * EVKHIP_ERR_UNSUPPORTED before launching anything.  Every call on one GPU
+ * shares that array and clears the counters it uses: calls that overlap on
+ * one GPU (on different streams) race. */
+#define EVKHIP_NOALLOC_PART_BYTES (8u << 20)
+int evkhip_matmul_noalloc(const evkhip_tensor* a, const evkhip_tensor* b, const evkhip_tensor* c,
+                          int transpose_a, int transpose_b, int acc_c,
+                          uint32_t tile_m, uint32_t tile_n, void* stream);
+
 /* evk::ai::flash_attention (evk_ai.h:497-501, evk_ai.cpp:332-369).
  * MQA: Q,O (B,N,H*Dh); K,V (B,N,Dh); H = D/Dh; scale 1/sqrt(Dh).
  * Extensions (defaults reproduce the reference): causal != 0 masks keys
