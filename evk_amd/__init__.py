@@ -72,6 +72,7 @@ SIGNATURES = {
     "evkhip_flash_attention_bwd": (C.c_int, [TP, TP, TP, TP, TP, TP, TP, TP, C.c_uint32, C.c_int,
                                              C.c_void_p, C.c_void_p]),
     "evkhip_single_query_attention": (C.c_int, [TP, TP, TP, TP, C.c_uint32, C.c_uint32, C.c_void_p]),
+    "evkhip_kv_cache_write": (C.c_int, [TP, TP, C.c_uint32, C.c_void_p]),
     "evkhip_rms_norm": (C.c_int, [TP, TP, C.c_float, C.c_void_p]),
     "evkhip_rope": (C.c_int, [TP, TP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32,
                               C.c_uint32, C.c_void_p]),
@@ -232,6 +233,11 @@ def single_query_attention(q, k_cache, v_cache, out, current_length, heads=1, st
                                                _ref(desc(v_cache)), _ref(desc(out)),
                                                int(current_length), int(heads), _stream(stream)))
     return out
+
+
+def kv_cache_write(src, cache, pos0, stream=None):
+    """Rows [pos0, pos0+n) of each sequence's cache (B, max_seq, D) <- src (B, n, D)."""
+    _check(lib().evkhip_kv_cache_write(_ref(desc(src)), _ref(desc(cache)), int(pos0), _stream(stream)))
 
 
 def rms_norm(inp, out, eps=1e-4, stream=None):

@@ -257,6 +257,28 @@ int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k
     CHECK(check_tensor(v_cache, "single_query_attention: v_cache", 2, EVKHIP_MAX_DIMS));
     CHECK(check_tensor(out, "single_query_attention: out", 1, EVKHIP_MAX_DIMS));
     EVK_RETURN_IF(heads == 0, EVKHIP_ERR_INVALID_ARG, "single_query_attention: heads must be >= 1");
+    // batched form: caches (B, max_len, D) with B > 1 and q, out holding B*D
+    const uint64_t cache_batch = k_cache->rank >= 3 ? batch_of(k_cache, 2) : 1;
+    if (cache_batch > 1) {
+        const uint64_t Dc = dim_at(k_cache, -1), max_len = dim_at(k_cache, -2);
+        EVK_RETURN_IF(!same_shape(k_cache, v_cache), EVKHIP_ERR_SHAPE, "single_query_attention: caches differ");
+        EVK_RETURN_IF(numel(q) != cache_batch * Dc || numel(out) != cache_batch * Dc, EVKHIP_ERR_SHAPE,
+                      "single_query_attention: %llu cached sequences of %llu values need q and out of %llu values",
+                      (unsigned long long)cache_batch, (unsigned long long)Dc,
+                      (unsigned long long)(cache_batch * Dc));
+        EVK_RETURN_IF(Dc % heads, EVKHIP_ERR_SHAPE, "single_query_attention: %llu values not divisible by %u heads",
+                      (unsigned long long)Dc, heads);
+        EVK_RETURN_IF(current_length > max_len, EVKHIP_ERR_SHAPE,
+                      "single_query_attention: current_length %u exceeds the %llu cached rows", current_length,
+                      (unsigned long long)max_len);
+        EVK_RETURN_IF(cache_batch > 65535 / heads, EVKHIP_ERR_UNSUPPORTED, "single_query_attention: too many sequences");
+        const bool alb = aligned16(q->data) && aligned16(k_cache->data) && aligned16(v_cache->data) &&
+                         aligned16(out->data);
+        return sq_attention_launch((const f16*)q->data, (const f16*)k_cache->data, (const f16*)v_cache->data,
+                                   (f16*)out->data, (int64_t)Dc, (int)heads, (int)(Dc / heads),
+                                   (int)current_length, alb, as_stream(stream), (int)cache_batch,
+                                   (int64_t)(max_len * Dc));
+    }
     const uint64_t D = numel(q);
     EVK_RETURN_IF(D == 0 || D % heads, EVKHIP_ERR_SHAPE, "single_query_attention: q size %llu not divisible by %u heads",
                   (unsigned long long)D, heads);
@@ -274,6 +296,20 @@ int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k
     return sq_attention_launch((const f16*)q->data, (const f16*)k_cache->data, (const f16*)v_cache->data,
                                (f16*)out->data, (int64_t)D, (int)heads, (int)dh, (int)current_length, al,
                                as_stream(stream));
+}
+
+int evkhip_kv_cache_write(const evkhip_tensor* src, const evkhip_tensor* cache, uint32_t pos0, void* stream) {
+    CHECK(check_tensor(src, "kv_cache_write: src", 2, 3));
+    CHECK(check_tensor(cache, "kv_cache_write: cache", 2, 3));
+    const uint32_t B = src->rank == 3 ? src->dims[0] : 1, n = dim_at(src, -2), D = dim_at(src, -1);
+    const uint32_t Bc = cache->rank == 3 ? cache->dims[0] : 1, max_seq = dim_at(cache, -2);
+    EVK_RETURN_IF(Bc != B || dim_at(cache, -1) != D, EVKHIP_ERR_SHAPE,
+                  "kv_cache_write: src (%u,%u,%u) does not match cache (%u,%u,%u)", B, n, D, Bc, max_seq,
+                  dim_at(cache, -1));
+    EVK_RETURN_IF((uint64_t)pos0 + n > max_seq, EVKHIP_ERR_SHAPE,
+                  "kv_cache_write: rows %u..%u exceed the cache's %u", pos0, pos0 + n, max_seq);
+    return kv_cache_write_launch((const f16*)src->data, (f16*)cache->data, (int)B, (int)n, (int)D, (int)max_seq,
+                                 (int)pos0, as_stream(stream));
 }
 
 int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream) {

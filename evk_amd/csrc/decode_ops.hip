@@ -25,7 +25,8 @@ struct SqArgs {
     const f16* vc;
     f16* out;
     int64_t row_stride;  // elements between consecutive cache rows
-    int heads, L, chunk;
+    int64_t cache_bstride;  // elements between the caches of consecutive sequences
+    int heads, L, chunk;    // heads per sequence; grid.x = sequences * heads
     float scale_log2;
     float* part;         // [heads][nsplit][2 + DH]
     unsigned* counters;  // [heads]
@@ -41,7 +42,12 @@ __global__ __launch_bounds__(256) void sq_attention(SqArgs a) {
     __shared__ float s_m[4], s_w[4];
     __shared__ float s_o[4][DH];
     __shared__ unsigned s_last;
+    // h: (sequence, head) pair; q, out and the workspace are indexed by it,
+    // the caches by the sequence's cache and the head's columns
     const int h = blockIdx.x, split = blockIdx.y, nsplit = gridDim.y;
+    const int seq = h / a.heads, hc = h - seq * a.heads;
+    const f16* kc = a.kc + (int64_t)seq * a.cache_bstride + (int64_t)hc * DH;
+    const f16* vc = a.vc + (int64_t)seq * a.cache_bstride + (int64_t)hc * DH;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = tid % LPK, kslot = tid / LPK;
     const int j0 = split * a.chunk, j1 = min(a.L, j0 + a.chunk);
@@ -61,9 +67,9 @@ __global__ __launch_bounds__(256) void sq_attention(SqArgs a) {
         float s = -INFINITY;
         half8 vh;
         if (j < j1) {
-            const f16* kr = a.kc + (int64_t)j * a.row_stride + (int64_t)h * DH + sub * 8;
+            const f16* kr = kc + (int64_t)j * a.row_stride + sub * 8;
             half8 kh = *reinterpret_cast<const half8*>(kr);
-            vh = *reinterpret_cast<const half8*>(a.vc + (int64_t)j * a.row_stride + (int64_t)h * DH + sub * 8);
+            vh = *reinterpret_cast<const half8*>(vc + (int64_t)j * a.row_stride + sub * 8);
             float d = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) d += qv[e] * (float)kh[e];
@@ -156,12 +162,15 @@ __global__ __launch_bounds__(256) void sq_attention_scalar(SqArgs a, int dh) {
     float* qs = sh + a.L;
     __shared__ float s_red[256];
     const int h = blockIdx.x, tid = threadIdx.x;
+    const int seq = h / a.heads, hc = h - seq * a.heads;
+    const f16* kc = a.kc + (int64_t)seq * a.cache_bstride + (int64_t)hc * dh;
+    const f16* vc = a.vc + (int64_t)seq * a.cache_bstride + (int64_t)hc * dh;
     for (int d = tid; d < dh; d += 256) qs[d] = (float)a.q[(int64_t)h * dh + d];
     __syncthreads();
     const float inv = a.scale_log2;
     float mx = -INFINITY;
     for (int j = tid; j < a.L; j += 256) {
-        const f16* kr = a.kc + (int64_t)j * a.row_stride + (int64_t)h * dh;
+        const f16* kr = kc + (int64_t)j * a.row_stride;
         float s = 0.0f;
         for (int d = 0; d < dh; ++d) s += qs[d] * (float)kr[d];
         sc[j] = s * inv;
@@ -189,9 +198,27 @@ __global__ __launch_bounds__(256) void sq_attention_scalar(SqArgs a, int dh) {
     const float is = s_red[0] > 0.0f ? 1.0f / s_red[0] : 0.0f;
     for (int d = tid; d < dh; d += 256) {
         float acc = 0.0f;
-        for (int j = 0; j < a.L; ++j) acc += sc[j] * (float)a.vc[(int64_t)j * a.row_stride + (int64_t)h * dh + d];
+        for (int j = 0; j < a.L; ++j) acc += sc[j] * (float)vc[(int64_t)j * a.row_stride + d];
         a.out[(int64_t)h * dh + d] = (f16)(acc * is);
     }
+}
+
+// ---------------------------------------------------------------------------
+// KV-cache append: rows [pos0, pos0 + n) of each sequence's cache (max_seq, D)
+// take the rows of src (batch, n, D).  One thread per 8 values (16 bytes)
+// when D % 8 == 0 and both buffers are 16-byte aligned, else per value.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kv_write_k(const f16* src, f16* cache, int64_t total, int n, int D,
+                                                  int max_seq, int pos0, int vec) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int W = vec ? 8 : 1;
+    const int64_t e0 = i * W;  // element index in src
+    if (e0 >= total) return;
+    const int64_t row = e0 / D, col = e0 % D;
+    const int64_t b = row / n, r = row % n;
+    f16* dst = cache + (b * max_seq + pos0 + r) * D + col;
+    if (vec) *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src + e0);
+    else *dst = src[e0];
 }
 
 // ---------------------------------------------------------------------------
@@ -311,10 +338,13 @@ void decode_ops_free_workspace() {
 }
 
 int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, int64_t row_stride, int heads,
-                        int dh, int L, bool vec_ok, hipStream_t st) {
+                        int dh, int L, bool vec_ok, hipStream_t st, int batch, int64_t cache_bstride) {
     SqArgs a{};
     a.q = q; a.kc = kc; a.vc = vc; a.out = out;
     a.row_stride = row_stride; a.heads = heads; a.L = L;
+    a.cache_bstride = cache_bstride;
+    // from here on `heads` counts (sequence, head) pairs: one grid row each
+    heads *= batch;
     a.scale_log2 = (1.0f / sqrtf((float)dh)) * kLog2e;
     const bool vec = vec_ok && (dh == 16 || dh == 32 || dh == 64 || dh == 128) && (row_stride % 8 == 0);
     if (!vec) {
@@ -368,6 +398,18 @@ int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, in
     }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? EVKHIP_OK : check_hip(e, "sq_attention launch");
+}
+
+int kv_cache_write_launch(const f16* src, f16* cache, int batch, int n, int D, int max_seq, int pos0,
+                          hipStream_t st) {
+    const int64_t total = (int64_t)batch * n * D;
+    if (total == 0) return EVKHIP_OK;
+    const int vec = (D % 8 == 0) && aligned16(src) && aligned16(cache);
+    const int64_t threads = vec ? total / 8 : total;
+    hipLaunchKernelGGL(kv_write_k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, src, cache, total, n,
+                       D, max_seq, pos0, vec);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? EVKHIP_OK : check_hip(e, "kv_cache_write launch");
 }
 
 int rms_norm_launch(const f16* in, f16* out, int64_t rows, int D, float eps, hipStream_t st) {

@@ -111,6 +111,11 @@ void single_query_attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor&
           "single_query_attention");
 }
 
+void kv_cache_write(Tensor& src, Tensor& cache, uint32_t pos0) {
+    evkhip_tensor S = desc(src), C = desc(cache);
+    check(evkhip_kv_cache_write(&S, &C, pos0, stream()), "kv_cache_write");
+}
+
 void add(Tensor& a, Tensor& b, Tensor& c) {
     evkhip_tensor A = desc(a), B = desc(b), C = desc(c);
     check(evkhip_add(&A, &B, &C, stream()), "add");

@@ -59,8 +59,14 @@ int flash_status(uint32_t* flags, bool clear);
 void flash_set_spin_limit(uint32_t n);
 
 // ---- decode_ops.hip ----
+// batch sequences: q, out (batch, heads*dh); sequence b's cache rows start at
+// b * cache_bstride elements.
 int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, int64_t row_stride, int heads,
-                        int dh, int L, bool vec_ok, hipStream_t st);
+                        int dh, int L, bool vec_ok, hipStream_t st, int batch = 1, int64_t cache_bstride = 0);
+// Cache rows [pos0, pos0 + n) of each of `batch` caches (max_seq, D) take
+// the rows of src (batch, n, D).
+int kv_cache_write_launch(const f16* src, f16* cache, int batch, int n, int D, int max_seq, int pos0,
+                          hipStream_t st);
 int rms_norm_launch(const f16* in, f16* out, int64_t rows, int D, float eps, hipStream_t st);
 int rope_launch(const f16* in, f16* out, int B, int S, int E, float base, int pos0, int hd, hipStream_t st);
 int gelu_launch(const f16* in, f16* out, int64_t n, hipStream_t st);

@@ -360,8 +360,14 @@ void flash_attention_bwd(Tensor& q, Tensor& k, Tensor& v, Tensor& o, Tensor& dO,
 // Decode-step attention of one query over a KV cache:
 // out[h] = softmax(q[h] . K[0:L, h]^T / sqrt(dh)) . V[0:L, h]
 // q, out: (heads*dh); k_cache, v_cache: (max_len, heads*dh) row-major.
+// Batched: k_cache, v_cache (B, max_len, heads*dh) with B > 1 and q, out
+// (B, heads*dh) or (B, 1, heads*dh): sequence b attends over its own cache.
 void single_query_attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& out,
                             uint32_t current_length, uint32_t heads = 1);
+
+// KV-cache append: rows [pos0, pos0+n) of each sequence's cache
+// (B, max_seq, D) take the rows of src (B, n, D).
+void kv_cache_write(Tensor& src, Tensor& cache, uint32_t pos0);
 
 // c = a + b (evk_ai.h:521).
 void add(Tensor& a, Tensor& b, Tensor& c);
@@ -749,3 +755,150 @@ private:
         return *nodes.back();
     }
 };
+
+namespace evk::ai {
+
+// Weights of one CausalAttentionBlock (example/main_llm.cpp:494-547): the
+// Graph's own parameter tensors, read in place.
+struct DecoderLayer {
+    Tensor* w_q;  // (D, D)
+    Tensor* w_k;  // (D, D)
+    Tensor* w_v;  // (D, D)
+    Tensor* w_o;  // (D, D)
+    Tensor* w1;   // (D, hidden)
+    Tensor* w2;   // (hidden, D)
+};
+
+// KV-cached decoding of the model example/main_llm.cpp builds with Graph
+// ops (MeshTokenModel, :549-620): embed, then per layer
+// CausalAttentionBlock::forward (:528-546) -- rms_norm, the q/k/v
+// projections, rope over the full width with position = sequence index,
+// single-head causal attention, the output projection and residual,
+// rms_norm, W1, gelu, W2 and residual -- then rms_norm and the output
+// projection.  It replaces the full recompute of sample_autoregressive
+// (:622-654) for B sequences decoded together:
+//   prefill(tokens)  runs the prompt (B, n) once (MFMA GEMMs, causal flash
+//                    attention) and writes every layer's rope'd keys and
+//                    values into per-layer caches (B, max_seq, D);
+//   step(ids)        feeds one token per sequence at position cached():
+//                    single-query attention over the caches, logits (B,1,V)
+//                    of that position; evk::ai::greedy_sample(logits(), out,
+//                    0, token_base, token_count) then picks the next ids
+//                    with the reference's token sub-range.
+// The rounding points are those of the Graph (every op output fp16), so the
+// greedy ids match a full recompute except at near-ties of the logits.
+class KVCacheDecoder {
+public:
+    KVCacheDecoder(Tensor& token_emb, Tensor& w_out, std::vector<DecoderLayer> layers, uint32_t batch,
+                   uint32_t max_seq, float rope_base = 10000.0f, float eps = 1e-4f)
+        : emb_(token_emb), w_out_(w_out), layers_(std::move(layers)), B_(batch), S_(max_seq), base_(rope_base),
+          eps_(eps) {
+        D_ = token_emb.shape[1];
+        V_ = w_out.shape[1];
+        assert(!layers_.empty() && layers_[0].w1 && "KVCacheDecoder: no layers");
+        H_ = layers_[0].w1->shape[1];
+        assert(w_out.shape[0] == D_ && D_ % 2 == 0 && "KVCacheDecoder: shapes");
+        for (size_t l = 0; l < layers_.size(); ++l) {
+            k_cache_.emplace_back(std::make_unique<Tensor>(Shape({B_, S_, D_})));
+            v_cache_.emplace_back(std::make_unique<Tensor>(Shape({B_, S_, D_})));
+        }
+        // prefill work tensors at their largest shape, aliased down per call
+        for (auto* t : {&px_, &ph_, &pq_, &pk_, &pv_, &pqr_, &pkr_, &po_, &pt_, &px1_})
+            *t = std::make_unique<Tensor>(Shape({B_, S_, D_}));
+        pu_ = std::make_unique<Tensor>(Shape({B_, S_, H_}));
+        pg_ = std::make_unique<Tensor>(Shape({B_, S_, H_}));
+        for (auto* t : {&sx_, &sh_, &sq_, &sk_, &sv_, &sqr_, &skr_, &so_, &st_})
+            *t = std::make_unique<Tensor>(Shape({B_, D_}));
+        su_ = std::make_unique<Tensor>(Shape({B_, H_}));
+        sg_ = std::make_unique<Tensor>(Shape({B_, H_}));
+        logits_ = std::make_unique<Tensor>(Shape({B_, 1, V_}));
+    }
+
+    uint32_t cached() const { return len_; }
+    Tensor& logits() { return *logits_; }
+    Tensor& k_cache(uint32_t layer) { return *k_cache_[layer]; }
+    Tensor& v_cache(uint32_t layer) { return *v_cache_[layer]; }
+    void reset() { len_ = 0; }
+
+    // tokens (B, n) raw uint16 ids of positions [0, n); the caches must be
+    // empty (reset() discards what they hold).
+    void prefill(Tensor& tokens) {
+        assert(tokens.shape.rank() == 2 && tokens.shape[0] == B_ && "prefill: tokens (B, n)");
+        const uint32_t n = tokens.shape[1];
+        assert(len_ == 0 && n > 0 && n <= S_ && "prefill: from an empty cache, n <= max_seq");
+        auto a = [&](std::unique_ptr<Tensor>& t, uint32_t w) { return Tensor::alias(Shape({B_, n, w}), t->buffer); };
+        Tensor x = a(px_, D_), h = a(ph_, D_), q = a(pq_, D_), k = a(pk_, D_), v = a(pv_, D_);
+        Tensor qr = a(pqr_, D_), kr = a(pkr_, D_), o = a(po_, D_), t = a(pt_, D_), x1 = a(px1_, D_);
+        Tensor u = a(pu_, H_), g = a(pg_, H_);
+        embed(emb_, tokens, x);
+        for (size_t l = 0; l < layers_.size(); ++l) {
+            const DecoderLayer& w = layers_[l];
+            rms_norm(x, h, eps_);
+            matmul(h, *w.w_q, q);
+            matmul(h, *w.w_k, k);
+            matmul(h, *w.w_v, v);
+            rope(q, qr, B_, n, D_, base_);
+            rope(k, kr, B_, n, D_, base_);
+            kv_cache_write(kr, *k_cache_[l], 0);
+            kv_cache_write(v, *v_cache_[l], 0);
+            flash_attention(qr, kr, v, o, /*causal=*/true);
+            layer_tail(w, x, o, t, x1, h, u, g);
+        }
+        len_ = n;
+    }
+
+    // ids (B) or (B, 1) raw uint16: the token of every sequence at position
+    // cached().  Returns logits() (B, 1, V) of that position.
+    Tensor& step(Tensor& ids) {
+        assert(ids.shape.count() == B_ && "step: one id per sequence");
+        assert(len_ < S_ && "step: the caches are full");
+        const uint32_t pos = len_;
+        Tensor krow = Tensor::alias(Shape({B_, 1, D_}), skr_->buffer);
+        Tensor vrow = Tensor::alias(Shape({B_, 1, D_}), sv_->buffer);
+        embed(emb_, ids, *sx_);
+        for (size_t l = 0; l < layers_.size(); ++l) {
+            const DecoderLayer& w = layers_[l];
+            rms_norm(*sx_, *sh_, eps_);
+            matmul(*sh_, *w.w_q, *sq_);
+            matmul(*sh_, *w.w_k, *sk_);
+            matmul(*sh_, *w.w_v, *sv_);
+            rope(*sq_, *sqr_, B_, 1, D_, base_, pos);
+            rope(*sk_, *skr_, B_, 1, D_, base_, pos);
+            kv_cache_write(krow, *k_cache_[l], pos);
+            kv_cache_write(vrow, *v_cache_[l], pos);
+            single_query_attention(*sqr_, *k_cache_[l], *v_cache_[l], *so_, pos + 1, 1);
+            layer_tail(w, *sx_, *so_, *st_, *sx_, *sh_, *su_, *sg_);
+        }
+        rms_norm(*sx_, *sh_, eps_);
+        Tensor flat = Tensor::alias(Shape({B_, V_}), logits_->buffer);
+        matmul(*sh_, w_out_, flat);
+        len_ = pos + 1;
+        return *logits_;
+    }
+
+private:
+    // attention output o -> x1 = x + o Wo; x = x1 + gelu(rms_norm(x1) W1) W2
+    void layer_tail(const DecoderLayer& w, Tensor& x, Tensor& o, Tensor& t, Tensor& x1, Tensor& h, Tensor& u,
+                    Tensor& g) {
+        matmul(o, *w.w_o, t);
+        add(x, t, x1);
+        rms_norm(x1, h, eps_);
+        matmul(h, *w.w1, u);
+        gelu(u, g);
+        matmul(g, *w.w2, t);
+        add(x1, t, x);
+    }
+
+    Tensor& emb_;
+    Tensor& w_out_;
+    std::vector<DecoderLayer> layers_;
+    uint32_t B_, S_, D_ = 0, V_ = 0, H_ = 0;
+    float base_, eps_;
+    uint32_t len_ = 0;
+    std::vector<std::unique_ptr<Tensor>> k_cache_, v_cache_;
+    std::unique_ptr<Tensor> px_, ph_, pq_, pk_, pv_, pqr_, pkr_, po_, pt_, px1_, pu_, pg_;
+    std::unique_ptr<Tensor> sx_, sh_, sq_, sk_, sv_, sqr_, skr_, so_, st_, su_, sg_;
+    std::unique_ptr<Tensor> logits_;
+};
+
+}  // namespace evk::ai

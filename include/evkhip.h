@@ -136,6 +136,16 @@ int evkhip_flash_attention_bwd(const evkhip_tensor* q, const evkhip_tensor* k,
 int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k_cache,
                                   const evkhip_tensor* v_cache, const evkhip_tensor* out,
                                   uint32_t current_length, uint32_t heads, void* stream);
+/* Batched form of the same entry (B sequences decoded together, e.g. the
+ * B = 16 of example/main_llm.cpp:622-654): caches (B, max_len, D) with B > 1,
+ * q and out (B, D) or (B, 1, D); sequence b attends over rows
+ * [0, current_length) of its own cache. */
+
+/* KV-cache append (no reference counterpart; the reference recomputes the
+ * whole sequence instead, main_llm.cpp:622-654): rows [pos0, pos0 + n) of
+ * each sequence's cache take that sequence's rows of src.
+ * src (B, n, D) or (n, D); cache (B, max_seq, D) or (max_seq, D). */
+int evkhip_kv_cache_write(const evkhip_tensor* src, const evkhip_tensor* cache, uint32_t pos0, void* stream);
 
 /* evk::ai::rms_norm (evk_ai.h:610, evk_ai.cpp:1045-1067, rms_norm.comp). */
 int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream);

@@ -841,6 +841,102 @@ static void test_graph_tiny_lm() {
     TEST(std::isfinite(last) && last < 0.7f * first);
 }
 
+// KV-cached decoding (evk::ai::KVCacheDecoder) of the model
+// example/main_llm.cpp trains -- B=16, seq 160, vocab 144, D=256, hidden
+// 512, 8 layers of CausalAttentionBlock, rope base 10000 -- against the
+// reference's own sampling loop (sample_autoregressive, :622-654): the full
+// Graph::eval over the (B, 160) token matrix plus greedy_sample at `pos`
+// over the coordinate tokens [3, 131).  Prefix: BOS + 18 tokens; 32 decode
+// steps, teacher-forced with the recompute's ids so one near-tie cannot
+// derail the rest.  Ids must agree except where the recompute's logits of
+// the two ids differ by less than 1e-3; logits agree within 3e-2.
+static void test_kv_decoder_matches_full_recompute() {
+    std::printf("test_kv_decoder_matches_full_recompute()\n");
+    const uint32_t B = 16, S = 160, V = 144, D = 256, HID = 512, L = 8, PREFIX = 19, STEPS = 32;
+    const uint16_t BASE = 3, BINS = 128;
+    Graph g;
+    Tensor& in = g.tensor({B, S});
+    Tensor& emb = g.tensor({V, D}, true);
+    Tensor* x = &g.embed(emb, in);
+    std::vector<evk::ai::DecoderLayer> layers(L);
+    srand(42);
+    emb.random_init(0.02f);
+    for (uint32_t l = 0; l < L; ++l) {
+        evk::ai::DecoderLayer& w = layers[l];
+        w.w_q = &g.tensor({D, D}, true).random_init(0.02f);
+        w.w_k = &g.tensor({D, D}, true).random_init(0.02f);
+        w.w_v = &g.tensor({D, D}, true).random_init(0.02f);
+        w.w_o = &g.tensor({D, D}, true).random_init(0.02f / std::sqrt(2.0f * L));
+        w.w1 = &g.tensor({D, HID}, true).random_init(0.02f);
+        w.w2 = &g.tensor({HID, D}, true).random_init(0.02f / std::sqrt(2.0f * L));
+        // CausalAttentionBlock::forward (main_llm.cpp:528-546)
+        Tensor& nin = g.rms_norm(*x);
+        Tensor& q = g.rope(g.matmul(nin, *w.w_q), 10000.0f);
+        Tensor& k = g.rope(g.matmul(nin, *w.w_k), 10000.0f);
+        Tensor& v = g.matmul(nin, *w.w_v);
+        Tensor& res1 = g.residual(*x, g.matmul(g.causal_attention(q, k, v), *w.w_o));
+        Tensor& hid = g.gelu(g.matmul(g.rms_norm(res1), *w.w1));
+        x = &g.residual(res1, g.matmul(hid, *w.w2));
+    }
+    Tensor& w_out = g.tensor({D, V}, true).random_init(0.02f);
+    Tensor& logits = g.matmul(g.rms_norm(*x), w_out, 16, 16);
+
+    std::vector<uint16_t> toks(B * S, 0);
+    Lcg rng(77);
+    for (uint32_t b = 0; b < B; ++b) {
+        toks[b * S] = 1;  // BOS
+        for (uint32_t i = 1; i < PREFIX; ++i)
+            toks[b * S + i] = uint16_t(BASE + uint32_t((rng.uniform() + 1.0f) * 0.5f * BINS) % BINS);
+    }
+    auto put_ids = [](Tensor& t, const uint16_t* src) {
+        float16_t* h = t.cpu();
+        for (uint32_t i = 0; i < t.shape.count(); ++i) h[i].value = src[i];
+        t.cpu_upload();
+    };
+    evk::ai::KVCacheDecoder dec(emb, w_out, layers, B, S);
+    Tensor prompt({B, PREFIX - 1});
+    {
+        std::vector<uint16_t> p(B * (PREFIX - 1));
+        for (uint32_t b = 0; b < B; ++b)
+            for (uint32_t i = 0; i + 1 < PREFIX; ++i) p[b * (PREFIX - 1) + i] = toks[b * S + i];
+        put_ids(prompt, p.data());
+    }
+    dec.prefill(prompt);
+    Tensor ids({B}), kv_next({B}), ref_next({B});
+    int mismatches = 0, ties = 0;
+    float max_dlogit = 0.0f;
+    for (uint32_t pos = PREFIX - 1; pos < PREFIX - 1 + STEPS; ++pos) {
+        // reference: full recompute over every position, sample at pos
+        put_ids(in, toks.data());
+        g.eval(false);
+        evk::ai::greedy_sample(logits, ref_next, pos, BASE, BINS);
+        // KV cache: one token per sequence at pos
+        std::vector<uint16_t> cur(B);
+        for (uint32_t b = 0; b < B; ++b) cur[b] = toks[b * S + pos];
+        put_ids(ids, cur.data());
+        Tensor& lg = dec.step(ids);
+        evk::ai::greedy_sample(lg, kv_next, 0, BASE, BINS);
+        std::vector<float> ref_l = download(logits), kv_l = download(lg);
+        ref_next.cpu_download();
+        kv_next.cpu_download();
+        for (uint32_t b = 0; b < B; ++b) {
+            const uint16_t r = ref_next.cpu()[b].value, k = kv_next.cpu()[b].value;
+            const float* rl = &ref_l[(size_t(b) * S + pos) * V];
+            for (uint32_t j = 0; j < V; ++j) max_dlogit = std::fmax(max_dlogit, std::fabs(rl[j] - kv_l[b * V + j]));
+            if (r != k) {
+                if (std::fabs(rl[r] - rl[k]) < 1e-3f) ++ties;
+                else ++mismatches;
+            }
+            toks[b * S + pos + 1] = r;  // teacher forcing with the recompute's id
+        }
+    }
+    std::printf("  %u steps x %u sequences: %d mismatches, %d near-ties, max |dlogit| %.4g\n", STEPS, B,
+                mismatches, ties, max_dlogit);
+    TEST(dec.cached() == PREFIX - 1 + STEPS);
+    TEST(mismatches == 0);
+    TEST(max_dlogit < 3e-2f);
+}
+
 static void test_timestamps() {
     std::printf("test_timestamps()\n");
     const uint32_t n = 1024;
@@ -921,6 +1017,7 @@ int main(int argc, char** argv) {
     test_graph_regression();
     test_graph_causal_attention_fused_vs_unfused();
     test_graph_tiny_lm();
+    test_kv_decoder_matches_full_recompute();
     test_timestamps();
     evk::ai::shutdown();
     std::printf("ALL PASSED\n");

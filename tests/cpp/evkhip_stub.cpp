@@ -106,6 +106,9 @@ int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k
                                   const evkhip_tensor* out, uint32_t L, uint32_t heads, void* stream) {
     return record("single_query_attention", {q, kc, vc, out}, {L, heads}, {}, stream);
 }
+int evkhip_kv_cache_write(const evkhip_tensor* src, const evkhip_tensor* cache, uint32_t pos0, void* stream) {
+    return record("kv_cache_write", {src, cache}, {pos0}, {}, stream);
+}
 int evkhip_rms_norm(const evkhip_tensor* in, const evkhip_tensor* out, float eps, void* stream) {
     return record("rms_norm", {in, out}, {}, {eps}, stream);
 }

@@ -283,3 +283,36 @@ def test_flash_forward_nan_input_propagates(dev, orc):
         got, want = g[0][mask], w[0][mask]
         assert np.all(np.isfinite(got))
         assert np.abs(got - want).max() <= 1e-2 + 1e-2 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("B,D,heads,L", [(16, 256, 1, 160), (3, 128, 2, 700), (4, 64, 1, 33), (2, 48, 1, 90)])
+def test_sq_attention_batched(dev, orc, B, D, heads, L):
+    """Batched single-query attention (B sequences, each over its own cache
+    (max_len, D)) against the oracle run per sequence; B=16, D=256, L=160 is
+    the decode shape of example/main_llm.cpp."""
+    import evk_amd as evk
+    maxlen = L + 7
+    q = orc.normal_f16((B, 1, D), 261 + L)
+    kc = orc.normal_f16((B, maxlen, D), 262 + L)
+    vc = orc.normal_f16((B, maxlen, D), 263 + L)
+    got = sq(evk, dev, q, kc, vc, L, heads).reshape(B, D)
+    for b in range(B):
+        want = orc.sq_attention(q[b], kc[b], vc[b], L, heads)
+        assert_close_f16(got[b], want, what=f"sq batched b={b}")
+
+
+def test_kv_cache_write(dev, orc):
+    """Rows [pos0, pos0 + n) of every sequence's cache take src; the rest of
+    the cache is untouched (bit-exact), for the vector and the scalar path."""
+    import torch
+    import evk_amd as evk
+    for D in (256, 36):
+        B, S, n, pos0 = 3, 50, 7, 20
+        src = orc.normal_f16((B, n, D), 271 + D)
+        cache = orc.normal_f16((B, S, D), 272 + D)
+        C = to_dev(cache, dev)
+        evk.kv_cache_write(to_dev(src, dev), C, pos0)
+        torch.cuda.synchronize()
+        want = cache.copy()
+        want[:, pos0:pos0 + n] = src
+        assert np.array_equal(from_dev(C), want)
