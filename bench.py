@@ -33,6 +33,10 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 METRIC = "fp16 GEMM & flash-attn fwd/bwd TFLOP/s (% MFMA peak); decode tok/s, GB/s"
+# --only names, one workload each (profiling runs take one at a time so that
+# a kernel-trace summary never mixes shapes under one kernel name)
+WORKLOADS = ["flash_fwd", "gemm_1024", "gemm_4096", "gemm_qkv", "gemv_m1", "gemv_m4", "gemv_m16", "flash_bwd",
+             "decode", "train_adam", "train_ce", "train_softmax", "graph_attn"]
 
 
 def parse():
@@ -42,7 +46,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-extras", action="store_true", help="headline only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--only", default="", help="comma list of secondary workloads to run")
+    p.add_argument("--only", default="", help="comma list of workloads to run (WORKLOADS); the headline "
+                   "fields are NaN unless flash_fwd is among them")
     p.add_argument("--profile-copy", action="store_true",
                    help="only run a plain 64 MiB device-to-device copy (HBM counter calibration)")
     return p.parse_args()
@@ -127,6 +132,107 @@ def read_traffic(name):
     return None
 
 
+def cpu_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return model, cores
+
+
+def cpu_baselines(orc, q, k, v, flops_c2):
+    """The reference's CPU path (a host fp32 implementation of the same ops,
+    example/tests.h:52-68 for the matmul) restated in oracle/oracle.c, timed
+    on this host: one thread (the reference's CPU code is single-threaded)
+    and all the cores this process may use (OpenMP).  Workloads too long for
+    a few seconds are timed on a slice and scaled linearly; `sample` says
+    which.  The headline fields are the C2 single-thread figure."""
+    import numpy as np
+    lib = orc.lib()
+    model, cores = cpu_info()
+
+    def clock(fn, threads):
+        lib.orc_set_threads(threads)
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    per = {}
+
+    def record(name, fn, work, unit, sample, threads_list=(1, cores), scale=1.0):
+        # work: units of `unit` done by one fn() call; scale: full / slice
+        entry = {"unit": unit, "sample": sample}
+        for t in threads_list:
+            dt = clock(fn, t)
+            entry[f"value_{t}t" if t != 1 else "value_1t"] = round(work / dt, 6)
+            entry[f"seconds_{t}t"] = round(dt, 3)
+        if scale != 1.0:
+            entry["slice_of_full"] = round(1.0 / scale, 6)
+        per[name] = entry
+        return entry
+
+    # C2: the full headline workload
+    c2 = record("flash_fwd_c2", lambda: orc.attention_fwd(q, k, v, True), flops_c2 / 1e12, "TFLOP/s",
+                "full C2 (B=4,H=8,S=1024,Dh=64 causal), orc_attention_fwd (fp32 scores, fp64 softmax)")
+    # C1: the literal tests.h:52-68 loop (single thread) and the same sums in
+    # a cache-friendly loop order over all cores (orc_matmul)
+    a1 = orc.uniform_f16((1024, 1024), 101)
+    b1 = orc.uniform_f16((1024, 1024), 102)
+    record("gemm_1024_naive", lambda: orc.matmul(a1[:256], b1, naive=True), 2 * 256 * 1024**2 / 1e12, "TFLOP/s",
+           "rows 0..255 of C1 1024^3 through orc_matmul_naive, the r->n->k fp32 loop of example/tests.h:52-68; "
+           "the rate is per row, so the full call takes 4 times as long", threads_list=(1,), scale=4.0)
+    record("gemm_1024", lambda: orc.matmul(a1, b1), 2 * 1024**3 / 1e12, "TFLOP/s",
+           "full C1 1024^3 through orc_matmul (same fp32 sums, k-outer loop, OpenMP over rows)")
+    # C3: one batch of four (the per-batch work is identical), scaled x4
+    g1 = orc.normal_f16((1, 1024, 512), 204)
+    record("flash_bwd_c3", lambda: orc.attention_bwd(q[:1], k[:1], v[:1], g1, True), 2.5 * flops_c2 / 4 / 1e12,
+           "TFLOP/s", "batch 0 of C3 (1 of 4 identical batches), orc_attention_bwd; rate of the slice",
+           scale=4.0)
+    # C4: two decode steps at positions 1024, 1025 over a seeded synthetic
+    # KV cache (the 1024-token prefill itself would take minutes on a CPU)
+    ocfg = orc.model_cfg()
+    w = orc.model_weights(ocfg, seed=301, std=0.02)
+    cache = orc.normal_f16((lib.orc_model_cache_elems(__import__("ctypes").byref(ocfg)),), 303, 0.0, 0.5)
+    d, hid, V_ = 768, 3072, 32000
+    tok_bytes = 12 * (d * 3 * d + d * d + 2 * d * hid) * 2 + d * V_ * 2 + 12 * 2 * 1025.5 * d * 2
+
+    def dec2():
+        orc.model_step(ocfg, w, cache, 5, 1024)
+        orc.model_step(ocfg, w, cache, 7, 1025)
+
+    c4 = record("decode_c4", dec2, 2.0, "tokens/s",
+                "2 greedy steps at positions 1024-1025 of the C4 model over a seeded synthetic KV cache")
+    for key in [x for x in c4 if x.startswith("value_")]:
+        c4[key.replace("value", "GB/s")] = round(c4[key] * tok_bytes / 1e9, 3)
+    del w, cache
+    # C5: row slices of the naive loop (single thread), scaled by M
+    for name, (gm, gn, gk, rows) in {"gemm_4096": (4096, 4096, 4096, 8),
+                                     "gemm_qkv_8192x12288x4096": (8192, 12288, 4096, 4),
+                                     "gemv_m1_11008x4096": (1, 11008, 4096, 1),
+                                     "gemv_m16_11008x4096": (16, 11008, 4096, 4)}.items():
+        a5 = orc.uniform_f16((rows, gk), 501)
+        b5 = orc.uniform_f16((gk, gn), 502)
+        record(name + "_naive", lambda: orc.matmul(a5, b5, naive=True), 2.0 * rows * gn * gk / 1e12,
+               "TFLOP/s", f"rows 0..{rows - 1} of M={gm} through orc_matmul_naive (tests.h:52-68); the "
+               "rate is per row, so the full call takes M/rows times as long", threads_list=(1,),
+               scale=gm / rows)
+    lib.orc_set_threads(cores)
+    return {"value": c2["value_1t"], "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": "the full C2 workload (B=4,H=8,S=1024,Dh=64 causal) through oracle/oracle.c "
+                      f"orc_attention_fwd, fp32, one thread, {c2['seconds_1t']} s",
+            "all_cores": {"value": c2[f"value_{cores}t"], "cores": cores},
+            "cpu_model": model, "nproc": cores, "per_config": per}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -145,6 +251,16 @@ def main():
 
     dev = torch.device("cuda:0")
     evk.initialize()
+    only = set(filter(None, args.only.split(",")))
+    unknown = only - set(WORKLOADS)
+    if unknown:
+        print(f"bench.py: unknown --only workloads {sorted(unknown)}; choose from {WORKLOADS}", file=sys.stderr)
+        sys.exit(2)
+
+    def want(name):
+        if only:
+            return name in only
+        return name == "flash_fwd" or not args.no_extras
 
     def to_dev(x):
         return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.float16).to(dev)
@@ -159,9 +275,12 @@ def main():
     L = torch.empty((B, H, S), dtype=torch.float32, device=dev)
     flops = 2.0 * B * H * S * S * Dh
     torch.cuda.synchronize()
-    ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup,
-               check=lambda: (O, L))
-    tflops = flops / (ms * 1e-3) / 1e12
+    if want("flash_fwd"):
+        ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup,
+                   check=lambda: (O, L))
+        tflops = flops / (ms * 1e-3) / 1e12
+    else:  # a profiling run of other workloads only
+        ms, tflops = float("nan"), float("nan")
     traffic = read_traffic("flash_fwd_c2_traffic.txt")
 
     out = {
@@ -187,10 +306,6 @@ def main():
 
     # ---------------- secondary configurations ---------------------------
     sec = {}
-    only = set(filter(None, args.only.split(",")))
-
-    def want(name):
-        return not args.no_extras and (not only or name in only)
 
     def gemm(gm, gn, gk, seed, steps):
         a = to_dev(orc.uniform_f16((gm, gk), seed))
@@ -200,16 +315,16 @@ def main():
         del a, b, c
         return ms_
 
-    if want("gemm"):
-        for name, (gm, gn, gk, st) in {"gemm_1024": (1024, 1024, 1024, 200),
-                                       "gemm_4096": (4096, 4096, 4096, 30),
-                                       "gemm_qkv_8192x12288x4096": (8192, 12288, 4096, 10)}.items():
+    for key, name, (gm, gn, gk, st) in [("gemm_1024", "gemm_1024", (1024, 1024, 1024, 200)),
+                                        ("gemm_4096", "gemm_4096", (4096, 4096, 4096, 30)),
+                                        ("gemm_qkv", "gemm_qkv_8192x12288x4096", (8192, 12288, 4096, 10))]:
+        if want(key):
             ms_ = gemm(gm, gn, gk, 101, st)
             tf = 2.0 * gm * gn * gk / (ms_ * 1e-3) / 1e12
             sec[name] = {"ms": round(ms_, 4), "TFLOP/s": round(tf, 1),
                          "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
-    if want("gemv"):
-        for gm in (1, 4, 16):
+    for gm in (1, 4, 16):
+        if want(f"gemv_m{gm}"):
             ms_ = gemm(gm, 11008, 4096, 501, 200)
             gbs = (4096 * 11008 + gm * 4096 + gm * 11008) * 2 / (ms_ * 1e-3) / 1e9
             sec[f"gemv_m{gm}_11008x4096"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
@@ -251,9 +366,8 @@ def main():
                             "GB/s": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
                             "bytes_per_token": int(step_bytes)}
         del w, cache
-    if want("train"):
-        # training ops (HBM-bound) and the Graph's causal attention, fused
-        # flash against the reference's unfused chain
+    if want("train_adam"):
+        # training ops (HBM-bound)
         n_p = 64 << 20
         prm = to_dev(orc.uniform_f16((n_p,), 601))
         grd = to_dev(orc.normal_f16((n_p,), 602))
@@ -265,6 +379,7 @@ def main():
         sec["train_adam_64M"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
                                  "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
         del prm, grd, m_s, v_s
+    if want("train_ce"):
         P_, V_ = 8192, 32000
         lg = to_dev(orc.normal_f16((P_, V_), 603))
         tg = torch.from_numpy(orc.tokens_u16(P_, 604, V_).view(np.int16)).to(dev)
@@ -275,6 +390,7 @@ def main():
         sec["train_cross_entropy_8192x32000"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
                                                  "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
         del lg, gr
+    if want("train_softmax"):
         sm_in = to_dev(orc.normal_f16((32, 1024, 1024), 605))
         sm_out = torch.empty_like(sm_in)
         ms_ = timed(lambda: evk.softmax(sm_in, sm_out, 0.125), 50, 5, check=lambda: (sm_out,))
@@ -282,6 +398,9 @@ def main():
         sec["train_softmax_32x1024x1024"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
                                              "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
         del sm_in, sm_out
+    if want("graph_attn"):
+        # the Graph's causal attention: fused flash against the reference's
+        # unfused chain (evk_ai.h:961-1007)
         Bq, Nq, Dq = 4, 1024, 64
         qa = to_dev(orc.normal_f16((Bq, Nq, Dq), 606))
         ka = to_dev(orc.normal_f16((Bq, Nq, Dq), 607))
@@ -319,18 +438,9 @@ def main():
     if sec:
         out["secondary"] = sec
 
-    # ---------------- CPU baseline (oracle port, single thread) ----------
+    # ---------------- CPU baseline (the oracle's C restatement) -----------
     if not args.no_cpu:
-        lib = orc.lib()
-        lib.orc_set_threads(1)
-        t0 = time.perf_counter()
-        orc.attention_fwd(q, k, v, True)
-        dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-                               "kind": "port",
-                               "sample": "the full C2 workload (B=4,H=8,S=1024,Dh=64 causal) through "
-                                         "oracle/oracle.c orc_attention_fwd, fp32, one thread, "
-                                         f"{dt:.1f} s"}
+        out["cpu_baseline"] = cpu_baselines(orc, q, k, v, flops)
     print(json.dumps(out))
 
 
