@@ -400,41 +400,44 @@ def main():
         del sm_in, sm_out
     if want("graph_attn"):
         # the Graph's causal attention: fused flash against the reference's
-        # unfused chain (evk_ai.h:961-1007)
-        Bq, Nq, Dq = 4, 1024, 64
-        qa = to_dev(orc.normal_f16((Bq, Nq, Dq), 606))
-        ka = to_dev(orc.normal_f16((Bq, Nq, Dq), 607))
-        va = to_dev(orc.normal_f16((Bq, Nq, Dq), 608))
-        ga = to_dev(orc.normal_f16((Bq, Nq, Dq), 609))
-        oa, la = torch.empty_like(qa), torch.empty((Bq, 1, Nq), dtype=torch.float32, device=dev)
-        dqa, dka, dva = torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+        # unfused chain (evk_ai.h:961-1007), single head, at two shapes: a
+        # long-sequence one and the one example/main_llm.cpp trains
+        # (B=16, N=160, D=256, :694-702)
+        for tag, (Bq, Nq, Dq, st_) in {"4x1024x64": (4, 1024, 64, 50), "16x160x256": (16, 160, 256, 100)}.items():
+            qa = to_dev(orc.normal_f16((Bq, Nq, Dq), 606))
+            ka = to_dev(orc.normal_f16((Bq, Nq, Dq), 607))
+            va = to_dev(orc.normal_f16((Bq, Nq, Dq), 608))
+            ga = to_dev(orc.normal_f16((Bq, Nq, Dq), 609))
+            oa, la = torch.empty_like(qa), torch.empty((Bq, 1, Nq), dtype=torch.float32, device=dev)
+            dqa, dka, dva = torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+            sm = 1.0 / float(np.sqrt(Dq))
 
-        def fused():
-            evk.flash_attention(qa, ka, va, oa, causal=True, lse=la)
-            evk.flash_attention_bwd(qa, ka, va, oa, ga, dqa, dka, dva, heads=1, causal=True, lse=la)
+            def fused():
+                evk.flash_attention(qa, ka, va, oa, causal=True, lse=la)
+                evk.flash_attention_bwd(qa, ka, va, oa, ga, dqa, dka, dva, heads=1, causal=True, lse=la)
 
-        ms_f = timed(fused, 50, 5, check=lambda: (oa, dqa, dka, dva))
-        sc_ = torch.empty((Bq, Nq, Nq), dtype=torch.float16, device=dev)
-        pr_, dp_, ds_ = torch.empty_like(sc_), torch.empty_like(sc_), torch.empty_like(sc_)
-        ou_, dqu, dku, dvu = torch.empty_like(qa), torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
+            ms_f = timed(fused, st_, 5, check=lambda: (oa, dqa, dka, dva))
+            sc_ = torch.empty((Bq, Nq, Nq), dtype=torch.float16, device=dev)
+            pr_, dp_, ds_ = torch.empty_like(sc_), torch.empty_like(sc_), torch.empty_like(sc_)
+            ou_, dqu, dku, dvu = torch.empty_like(qa), torch.empty_like(qa), torch.empty_like(ka), torch.empty_like(va)
 
-        def unfused():  # Graph::causal_attention of the reference (evk_ai.h:961-1007)
-            evk.matmul(qa, ka, sc_, False, True)
-            evk.apply_causal_mask(sc_)
-            evk.softmax(sc_, pr_, 0.125)
-            evk.matmul(pr_, va, ou_)
-            evk.matmul(ga, va, dp_, False, True)
-            evk.matmul(pr_, ga, dvu, True, False)
-            ds_.zero_()
-            evk.softmax_backward(pr_, dp_, ds_, 0.125)
-            evk.matmul(ds_, ka, dqu)
-            evk.matmul(ds_, qa, dku, True, False)
+            def unfused():
+                evk.matmul(qa, ka, sc_, False, True)
+                evk.apply_causal_mask(sc_)
+                evk.softmax(sc_, pr_, sm)
+                evk.matmul(pr_, va, ou_)
+                evk.matmul(ga, va, dp_, False, True)
+                evk.matmul(pr_, ga, dvu, True, False)
+                ds_.zero_()
+                evk.softmax_backward(pr_, dp_, ds_, sm)
+                evk.matmul(ds_, ka, dqu)
+                evk.matmul(ds_, qa, dku, True, False)
 
-        ms_u = timed(unfused, 20, 3, check=lambda: (ou_, dqu, dku, dvu))
-        sec["graph_causal_attention_4x1024x64_fwd_bwd"] = {
-            "fused_flash_ms": round(ms_f, 4), "unfused_ms": round(ms_u, 4),
-            "speedup": round(ms_u / ms_f, 2)}
-        del qa, ka, va, ga, oa, dqa, dka, dva, sc_, pr_, dp_, ds_, ou_, dqu, dku, dvu
+            ms_u = timed(unfused, max(20, st_ // 2), 3, check=lambda: (ou_, dqu, dku, dvu))
+            sec[f"graph_causal_attention_{tag}_fwd_bwd"] = {
+                "fused_flash_ms": round(ms_f, 4), "unfused_ms": round(ms_u, 4),
+                "speedup": round(ms_u / ms_f, 2)}
+            del qa, ka, va, ga, oa, dqa, dka, dva, sc_, pr_, dp_, ds_, ou_, dqu, dku, dvu
     if sec:
         out["secondary"] = sec
 

@@ -21,7 +21,8 @@ BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("EVK_OFFLOAD_ARCH", "gfx950")
 
-KERNEL_SOURCES = ["capi.hip", "gemm.hip", "flash.hip", "decode_ops.hip", "model.hip", "train_ops.hip"]
+KERNEL_SOURCES = ["capi.hip", "gemm.hip", "flash.hip", "flash_wide.hip", "decode_ops.hip", "model.hip",
+                  "train_ops.hip"]
 API_SOURCES = ["evk_runtime.cpp", "evk_ai.cpp"]
 
 HIP_FLAGS = [
@@ -41,7 +42,7 @@ def _run(cmd):
 
 # Files whose MFMA accumulators fit in the architectural VGPRs: keep them there
 # (no AGPR<->VGPR copies around the softmax / epilogue arithmetic).
-VGPR_MFMA = {"flash.hip"}
+VGPR_MFMA = {"flash.hip", "flash_wide.hip"}
 
 
 def _compile(src: str) -> str:

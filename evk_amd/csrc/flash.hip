@@ -1815,6 +1815,7 @@ int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
     if (mfma && dh == 32) e = launch_fwd<32>(a, causal, 0, st);
     else if (mfma && dh == 64) e = launch_fwd<64>(a, causal, 0, st);
     else if (mfma && dh == 128) e = launch_fwd<128>(a, causal, 0, st);
+    else if (mfma && flash_wide_head(dh)) e = flash_forward_wide(a, dh, causal, st);
     else {
         dim3 g((unsigned)(((int64_t)a.B * a.N * a.H + 63) / 64));
         hipLaunchKernelGGL(flash_fwd_scalar, g, dim3(64), 0, st, a, dh, (int)causal, 0);
@@ -1829,16 +1830,17 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
     a.scale_log2 = a.scale * kLog2e;
     const size_t rows = (size_t)a.B * a.N * a.H;
     const bool have_lse = a.lse != nullptr;
-    const bool split = mfma && dh <= 64 && (int64_t)a.N * a.H * dh * 2 < (int64_t)INT32_MAX;
+    const bool split = mfma && dh <= 64 && !flash_wide_head(dh) && (int64_t)a.N * a.H * dh * 2 < (int64_t)INT32_MAX;
+    const bool wide = mfma && flash_wide_head(dh);
     // arena layout (256-byte aligned pieces)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const int nkb = (a.N + BKB - 1) / BKB;
     int parts_per_batch = 0;
     if (split)
         for (int kb = 0; kb < nkb; ++kb) parts_per_batch += bwd_kv_parts(kb, a.N, a.H, causal);
-    const size_t stats_b = split ? 0 : al(2 * rows * sizeof(float));  // split: formed in-kernel
+    const size_t stats_b = (split || wide) ? 0 : al(2 * rows * sizeof(float));  // formed in-kernel
     const size_t part_b = split ? al((size_t)a.B * parts_per_batch * 4 * (2 * 2 * (dh / 16)) * 64 * 16) : 0;
-    const size_t fwd_b = (split && !have_lse) ? al(rows * dh * 2) + al(rows * sizeof(float)) : 0;
+    const size_t fwd_b = ((split || wide) && !have_lse) ? al(rows * dh * 2) + al(rows * sizeof(float)) : 0;
     const size_t need = stats_b + part_b + fwd_b;
     if (need > g_bwd_ws_bytes) {
         if (g_bwd_ws) EVK_HIP(hipFree(g_bwd_ws));
@@ -1866,6 +1868,18 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
         }
         e = (dh == 32) ? launch_bwd_split<32>(a, causal, parts, parts_per_batch, st)
                        : launch_bwd_split<64>(a, causal, parts, parts_per_batch, st);
+    } else if (wide) {
+        if (!have_lse) {
+            // recompute the forward's O and LSE into the arena
+            FlashArgs f = a;
+            f.out = reinterpret_cast<f16*>(g_bwd_ws + stats_b);
+            f.lse = reinterpret_cast<float*>(g_bwd_ws + stats_b + al(rows * dh * 2));
+            e = flash_forward_wide(f, dh, causal, st);
+            if (e != hipSuccess) return check_hip(e, "flash backward: forward recompute");
+            a.o = f.out;
+            a.lse = f.lse;
+        }
+        e = flash_backward_wide(a, dh, causal, st);
     } else if (mfma && dh == 32) {
         e = launch_bwd<32>(a, causal, have_lse, st);
     } else if (mfma && dh == 64) {

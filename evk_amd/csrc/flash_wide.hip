@@ -1,0 +1,583 @@
+// Flash attention forward / backward on the MFMA for head sizes the
+// specialised kernels of flash.hip do not cover: any multiple of 16 up to
+// 256 (the reference's flash shader takes Dh <= 256, flash_attention.comp:46;
+// its only training caller runs one head of 256, example/main_llm.cpp:694-702
+// through Graph::causal_attention, evk_ai.h:961-1007).
+//
+// Layout as in flash.hip (reference MQA): Q,O,dO,dQ (B,N,H*Dh); K,V,dK,dV
+// (B,N,Dh); per batch the query side is an (N*H) x Dh matrix whose row r is
+// position r/H of head r%H.
+//
+// MFMA forms (lane l, g = l/16, l16 = l%16):
+//   v_mfma_f32_16x16x16_f16 for contractions over Dh (16 per step):
+//       A row l16, B column l16, k = 4g..4g+3; D column l16, rows 4g+j.
+//   v_mfma_f32_16x16x32_f16 for contractions over 32 keys or 32 rows:
+//       operand slot s of lane l holds k = 4g+s (s < 4) or 16+4g+s-4, which
+//       is exactly how two 16-wide D blocks lay out their rows, so
+//       probabilities go from one MFMA's result to the next one's operand
+//       without moving; the other operand comes from a row-major LDS tile
+//       through ds_read_b64_tr_b16 (rows 4g.. and 16+4g.., 16 columns).
+// Every score is scaled in fp32 (s * scale * log2(e), exp2 domain).
+#include "kernels.h"
+
+#include <math.h>
+
+namespace evkhip {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int WKC = 32;   // keys (or rows) per chunk
+
+DEV floatx4 mfma_k16(const half4& a, const half4& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+DEV half8 pack_slots(const floatx4& x0, const floatx4& x1) {
+    u32x4 u = {pack_h2(x0[0], x0[1]), pack_h2(x0[2], x0[3]), pack_h2(x1[0], x1[1]), pack_h2(x1[2], x1[3])};
+    return as_half8(u);
+}
+
+// WKC rows x DH halves of a (rows, DH) row-major matrix, loaded into
+// registers by the workgroup's 256 threads and stored into an LDS tile with
+// rows of DH + 8 halves (the next tile's loads fly during the current one).
+// Rows outside the buffer descriptor read as zeros.
+template <int DH>
+struct WideTile {
+    static constexpr int W = DH + 8;
+    static constexpr int PIECES = WKC * DH / 8;  // 16-byte pieces
+    static constexpr int PER = (PIECES + 255) / 256;
+    u32x4 r[PER];
+    DEV void load(__amdgpu_buffer_rsrc_t res, int row0) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            const int row = pc / (DH / 8), col = (pc % (DH / 8)) * 8;
+            const bool ok = PIECES % 256 == 0 || pc < PIECES;
+            r[i] = buf_load16(res, oob_or(ok, (uint32_t)((row0 + row) * DH + col) * 2u), 0);
+        }
+    }
+    DEV void store(f16* lds) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            if (PIECES % 256 == 0 || pc < PIECES) {
+                const int row = pc / (DH / 8), col = (pc % (DH / 8)) * 8;
+                *reinterpret_cast<u32x4*>(lds + row * W + col) = r[i];
+            }
+        }
+    }
+};
+
+// 4 halves at element `elem` through a buffer descriptor (zeros unless ok)
+DEV half4 ld_h4(__amdgpu_buffer_rsrc_t res, bool ok, int elem) {
+    const uint32_t off = oob_or(ok, (uint32_t)elem * 2u);
+    return __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(res, off, 0, 0));
+}
+
+// A operand of a 16x16x32 MFMA from a row-major LDS tile (rows of W
+// halves): column c0 + l16 of rows {4g..4g+3, 16+4g..16+4g+3} (slot order).
+template <int W>
+DEV half8 tile_tr(const f16* t, int c0, int g, int trow, int tcol) {
+    const f16* base = t + (4 * g + trow) * W + c0 + tcol;
+    return cat4(lds_read_tr(base), lds_read_tr(base + 16 * W));
+}
+
+// NT independent 16 x 16 blocks of D = A B^T contracted over DH (16x16x16
+// steps): block t takes A rows r0[t] + l16 of LDS tile a[t] (rows of W
+// halves) and the B fragments bf[t] from registers; D element j: row
+// r0[t] + 4 g + j, column l16.  The blocks advance together (independent
+// accumulators keep the MFMA pipe busy) and the A fragments of step ks + 1
+// are requested before the MFMAs of step ks.
+template <int DH, int W, int NT>
+DEV void contract_dh(const f16* const (&a)[NT], const int (&r0)[NT], const half4* const (&bf)[NT], int l16, int g,
+                     floatx4 (&acc)[NT]) {
+    constexpr int KS = DH / 16;
+    const f16* row[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        row[t] = a[t] + (r0[t] + l16) * W + g * 4;
+        acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    half4 cur[NT], nxt[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) cur[t] = *reinterpret_cast<const half4*>(row[t]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) nxt[t] = *reinterpret_cast<const half4*>(row[t] + (ks + 1) * 16);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = mfma_k16(cur[t], bf[t][ks], acc[t]);
+        if (ks + 1 < KS) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) cur[t] = nxt[t];
+        }
+    }
+}
+
+// dh blocks (16 wide) of a wave when four waves share DB of them
+template <int DB>
+struct DhShare {
+    static constexpr int PER = (DB + 3) / 4;
+};
+
+// ---------------------------------------------------------------------------
+// Forward: O and the public LSE.  Grid (ceil(N*H/16), B), 4 waves per
+// workgroup for 16 query rows R0 + l16 (the B operand Q^T in registers).
+// K and V come in 32-key tiles staged in LDS for the workgroup (double
+// buffered).  Every wave forms the tile's scores and probabilities itself
+// (a 32 x 16 block, cheap next to loading the tile), and wave w multiplies
+// them into dh blocks w, w+4, ... of the output:
+//   S^T(16 keys x 16 q) = K Q^T   (DH/16 steps of 16x16x16)
+//   O^T(16 dh x 16 q) += V^T P^T  (16x16x32, V^T by tr reads)
+//   row sums: ones . P^T on the MFMA.
+// Rescaling is lazy: a row's reference maximum moves only when a chunk has a
+// score more than 2^8 above it.
+// ---------------------------------------------------------------------------
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
+    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    __shared__ __attribute__((aligned(16))) f16 sK[2][WKC * W];
+    __shared__ __attribute__((aligned(16))) f16 sV[2][WKC * W];
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4, trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    const int R0 = blockIdx.x * 16;
+    const int myrow = R0 + l16;
+    const bool row_ok = myrow < NH;
+    const int qpos = min(myrow, NH - 1) / H;
+    const int pmax = min(R0 + 15, NH - 1) / H, pmin = R0 / H;
+    const int kend = CAUSAL ? min(N, pmax + 1) : N;
+    const float c2 = p.scale_log2;
+
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+
+    half4 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = ld_h4(qres, row_ok, myrow * DH + ks * 16 + g * 4);
+    // drain these loads here: inside the loop the only loads in flight are
+    // then the next tile's, which the loop waits for at its LDS store only
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+    floatx4 oacc[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) oacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 lacc = {0.f, 0.f, 0.f, 0.f};
+    float m_ref = -INFINITY;
+    const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
+
+    WideTile<DH> lk, lv;
+    const int nkt = (kend + WKC - 1) / WKC;
+    if (nkt > 0) {
+        lk.load(kres, 0);
+        lv.load(vres, 0);
+        lk.store(sK[0]);
+        lv.store(sV[0]);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nkt;
+        if (more) {
+            lk.load(kres, (kt + 1) * WKC);
+            lv.load(vres, (kt + 1) * WKC);
+        }
+        const int key0 = kt * WKC;
+        // element j of s[kb]: key key0 + 16 kb + 4 g + j, query myrow
+        floatx4 s[2];
+        contract_dh<DH, W, 2>({sK[cur], sK[cur]}, {0, 16}, {qf, qf}, l16, g, s);
+        if ((key0 + WKC > N) || (CAUSAL && key0 + WKC - 1 > pmin)) {
+            const int lim = (CAUSAL ? min(N - 1, qpos) : N - 1) - key0 - 4 * g;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[kb][j] = (kb * 16 + j > lim) ? -INFINITY : s[kb][j];
+        }
+        float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]))) * c2;
+        if (__any(mx > m_ref + 8.0f)) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_ref, mx);
+            const float alpha = (m_ref == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_ref - m_new);
+#pragma unroll
+            for (int i = 0; i < DPW; ++i) oacc[i] *= alpha;
+            lacc *= alpha;
+            m_ref = m_new;
+        }
+        const float nbase = (m_ref == -INFINITY) ? 0.0f : -m_ref;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s[kb][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c2, nbase));
+        const half8 pb = pack_slots(s[0], s[1]);
+        lacc = mfma16(ones8, pb, lacc);
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) {
+            const int d = wave + 4 * i;
+            if (DB % 4 == 0 || d < DB) oacc[i] = mfma16(tile_tr<W>(sV[cur], d * 16, g, trow, tcol), pb, oacc[i]);
+        }
+        if (more) {
+            lk.store(sK[cur ^ 1]);
+            lv.store(sV[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+    if (!row_ok) return;
+    const float l = lacc[0];
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    f16* orow = p.out + ((int64_t)b * NH + myrow) * DH;
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const int d = wave + 4 * i;
+        if (DB % 4 == 0 || d < DB) {
+            const u32x2 w2 = {pack_h2(oacc[i][0] * inv, oacc[i][1] * inv), pack_h2(oacc[i][2] * inv, oacc[i][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + d * 16 + g * 4) = w2;
+        }
+    }
+    if (p.lse && wave == 0 && g == 0)
+        p.lse[((int64_t)b * H + myrow % H) * N + qpos] = l > 0.0f ? (m_ref + log2f(l)) * kLn2 : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV (blocks of flash_bwd_wide).  4 waves; a workgroup owns 16 keys k0 + l16
+// (K^T, V^T as B-operand registers) and walks every query row at or after
+// k0 in 32-row tiles of Q and dO (with their lse2 and D) staged in LDS for
+// the workgroup, so the MQA sum over heads happens in the accumulation.
+// Every wave forms the tile's P and dS itself; wave w accumulates dh blocks
+// w, w+4, ... of dK and dV:
+//   S, dP (16 rows x 16 keys) = Q K^T, dO V^T  (16x16x16 over DH)
+//   P = 2^(S c - lse2_row), dS = P (dP - D_row)
+//   dV^T(16 dh x 16 keys) += dO^T P, dK^T += Q^T dS  (16x16x32 over rows)
+// ---------------------------------------------------------------------------
+// D = rowsum(dO * O) of a 32-row tile, any DH (a multiple of 16): thread t
+// takes row t / 8 and the half pairs 2 (t % 8) + 16 m of it (4-byte loads),
+// the 8 threads of a row (consecutive lanes) add up with shuffles.
+template <int DH>
+struct RowDot {
+    uint32_t o[DH / 16], g[DH / 16];
+    DEV void load(__amdgpu_buffer_rsrc_t ores, __amdgpu_buffer_rsrc_t gres, int row0, int nrows) {
+        const int row = row0 + (int)(threadIdx.x >> 3), c = 2 * (int)(threadIdx.x & 7);
+#pragma unroll
+        for (int m = 0; m < DH / 16; ++m) {
+            const uint32_t off = oob_or(row < nrows, (uint32_t)(row * DH + c + 16 * m) * 2u);
+            o[m] = __builtin_amdgcn_raw_buffer_load_b32(ores, off, 0, 0);
+            g[m] = __builtin_amdgcn_raw_buffer_load_b32(gres, off, 0, 0);
+        }
+    }
+    // the sum, in every lane of the row's eight
+    DEV float sum() const {
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < DH / 16; ++m) {
+            const half2_t a = __builtin_bit_cast(half2_t, o[m]), b = __builtin_bit_cast(half2_t, g[m]);
+            acc = __builtin_fmaf((float)a[0], (float)b[0], acc);
+            acc = __builtin_fmaf((float)a[1], (float)b[1], acc);
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        return acc;
+    }
+};
+
+// LDS of a flash_bwd_wide workgroup, either role: two double-buffered
+// 32-row tiles, then (dK/dV) the tiles' lse2 and D
+template <int DH>
+constexpr int bwd_wide_lds() { return 2 * 2 * WKC * WideTile<DH>::W * 2 + 2 * 2 * WKC * 4; }
+
+template <int DH, bool CAUSAL>
+__device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
+    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    f16 (*sQ)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds);
+    f16 (*sG)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds + 2 * WKC * W * 2);
+    float (*sL)[WKC] = reinterpret_cast<float (*)[WKC]>(lds + 4 * WKC * W * 2);
+    float (*sD)[WKC] = reinterpret_cast<float (*)[WKC]>(lds + 4 * WKC * W * 2 + 2 * WKC * 4);
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4, trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    const int k0 = bx * 16;
+    const int mykey = k0 + l16;
+    const bool key_ok = mykey < N;
+    const float c2 = p.scale_log2;
+
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const float* lse_b = p.lse + (int64_t)b * H * N;
+
+    half4 kf[KS], vf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        kf[ks] = ld_h4(kres, key_ok, mykey * DH + ks * 16 + g * 4);
+        vf[ks] = ld_h4(vres, key_ok, mykey * DH + ks * 16 + g * 4);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): see flash_fwd_wide
+    floatx4 dk[DPW], dv[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        dk[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // rows of positions >= k0 (causal), in tiles of 32
+    const int rstart = CAUSAL ? min(NH, k0 * H) / WKC * WKC : 0;
+    const int nrt = (NH - rstart + WKC - 1) / WKC;
+    // per row of a tile: lse2 = LSE * log2(e) of (position, head), and D
+    WideTile<DH> lq, lg;
+    RowDot<DH> rd;
+    float lsv = 0.0f;
+    auto load_stats = [&](int t) {
+        const int r0 = rstart + t * WKC;
+        rd.load(ores, gres, r0, NH);
+        const int r = r0 + (int)threadIdx.x;
+        lsv = (threadIdx.x < WKC && r < NH) ? lse_b[(r % H) * N + r / H] * kLog2e : 0.0f;
+    };
+    auto store_stats = [&](int st) {
+        const float d = rd.sum();
+        if ((threadIdx.x & 7) == 0) sD[st][threadIdx.x >> 3] = d;
+        if (threadIdx.x < WKC) sL[st][threadIdx.x] = lsv;
+    };
+    if (nrt > 0) {
+        lq.load(qres, rstart);
+        lg.load(gres, rstart);
+        load_stats(0);
+        lq.store(sQ[0]);
+        lg.store(sG[0]);
+        store_stats(0);
+    }
+    __syncthreads();
+    for (int rt = 0; rt < nrt; ++rt) {
+        const int cur = rt & 1;
+        const bool more = rt + 1 < nrt;
+        if (more) {
+            lq.load(qres, rstart + (rt + 1) * WKC);
+            lg.load(gres, rstart + (rt + 1) * WKC);
+            load_stats(rt + 1);
+        }
+        const int r0 = rstart + rt * WKC;
+        // element j of s[rb]: row r0 + 16 rb + 4 g + j, key mykey
+        floatx4 sd[4];  // S rows 0-15, 16-31, then dP
+        contract_dh<DH, W, 4>({sQ[cur], sQ[cur], sG[cur], sG[cur]}, {0, 16, 0, 16}, {kf, kf, vf, vf}, l16, g, sd);
+        const floatx4 s[2] = {sd[0], sd[1]}, dp[2] = {sd[2], sd[3]};
+        floatx4 pe[2], ds[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int rl = rb * 16 + 4 * g + j, r = r0 + rl;
+                const bool ok = r < NH && key_ok && (!CAUSAL || mykey <= r / H);
+                const float pv = ok ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][j], c2, -sL[cur][rl])) : 0.0f;
+                pe[rb][j] = pv;
+                ds[rb][j] = pv * (dp[rb][j] - sD[cur][rl]);
+            }
+        const half8 pb = pack_slots(pe[0], pe[1]), sb = pack_slots(ds[0], ds[1]);
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) {
+            const int d = wave + 4 * i;
+            if (DB % 4 == 0 || d < DB) {
+                dv[i] = mfma16(tile_tr<W>(sG[cur], d * 16, g, trow, tcol), pb, dv[i]);
+                dk[i] = mfma16(tile_tr<W>(sQ[cur], d * 16, g, trow, tcol), sb, dk[i]);
+            }
+        }
+        if (more) {
+            lq.store(sQ[cur ^ 1]);
+            lg.store(sG[cur ^ 1]);
+            store_stats(cur ^ 1);
+        }
+        __syncthreads();
+    }
+    if (!key_ok) return;
+    // element j of dk[i]: dh 16 d + 4 g + j of key mykey
+    f16* kdst = p.dK + ((int64_t)b * N + mykey) * DH;
+    f16* vdst = p.dV + ((int64_t)b * N + mykey) * DH;
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const int d = wave + 4 * i;
+        if (DB % 4 == 0 || d < DB) {
+            const u32x2 a = {pack_h2(dk[i][0] * p.scale, dk[i][1] * p.scale), pack_h2(dk[i][2] * p.scale, dk[i][3] * p.scale)};
+            const u32x2 c = {pack_h2(dv[i][0], dv[i][1]), pack_h2(dv[i][2], dv[i][3])};
+            *reinterpret_cast<u32x2*>(kdst + d * 16 + g * 4) = a;
+            *reinterpret_cast<u32x2*>(vdst + d * 16 + g * 4) = c;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ (blocks of flash_bwd_wide).  4 waves for 16 query rows (Q^T and dO^T as B
+// operands); K and V in 32-key tiles staged in LDS as in the forward; every
+// wave forms dS, wave w accumulates dh blocks w, w+4, ... of dQ:
+//   S^T, dP^T (16 keys x 16 q) = K Q^T, V dO^T  (16x16x16 over DH)
+//   dS^T = P^T (dP^T - D), P = 2^(S c - lse2_row)
+//   dQ^T(16 dh x 16 q) += K^T dS^T  (16x16x32 over keys, K^T by tr reads)
+// ---------------------------------------------------------------------------
+template <int DH, bool CAUSAL>
+__device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
+    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    f16 (*sK)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds);
+    f16 (*sV)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds + 2 * WKC * W * 2);
+
+    const int H = p.H, N = p.N, NH = N * H;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, g = lane >> 4, trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    const int R0 = bx * 16;
+    const int myrow = R0 + l16;
+    const bool row_ok = myrow < NH;
+    const int qpos = min(myrow, NH - 1) / H;
+    const int pmax = min(R0 + 15, NH - 1) / H, pmin = R0 / H;
+    const int kend = CAUSAL ? min(N, pmax + 1) : N;
+    const float c2 = p.scale_log2;
+
+    const __amdgpu_buffer_rsrc_t kres = buf_rsrc(p.k + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
+    const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
+    const float my_lse2 = row_ok ? p.lse[((int64_t)b * H + myrow % H) * N + qpos] * kLog2e : 0.0f;
+
+    half4 qf[KS], gf[KS];
+    float my_d = 0.0f;  // D = rowsum(dO * O): this lane's dh, then the row's four lane groups
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        qf[ks] = ld_h4(qres, row_ok, myrow * DH + ks * 16 + g * 4);
+        gf[ks] = ld_h4(gres, row_ok, myrow * DH + ks * 16 + g * 4);
+        const half4 of = ld_h4(ores, row_ok, myrow * DH + ks * 16 + g * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) my_d = __builtin_fmaf((float)of[e], (float)gf[ks][e], my_d);
+    }
+    my_d += __shfl_xor(my_d, 16, 64);
+    my_d += __shfl_xor(my_d, 32, 64);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): see flash_fwd_wide
+    floatx4 dq[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    WideTile<DH> lk, lv;
+    const int nkt = (kend + WKC - 1) / WKC;
+    if (nkt > 0) {
+        lk.load(kres, 0);
+        lv.load(vres, 0);
+        lk.store(sK[0]);
+        lv.store(sV[0]);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nkt;
+        if (more) {
+            lk.load(kres, (kt + 1) * WKC);
+            lv.load(vres, (kt + 1) * WKC);
+        }
+        const int key0 = kt * WKC;
+        floatx4 sd[4];  // S^T keys 0-15, 16-31, then dP^T
+        contract_dh<DH, W, 4>({sK[cur], sK[cur], sV[cur], sV[cur]}, {0, 16, 0, 16}, {qf, qf, gf, gf}, l16, g, sd);
+        const floatx4 s[2] = {sd[0], sd[1]}, dp[2] = {sd[2], sd[3]};
+        const bool need_mask = (key0 + WKC > N) || (CAUSAL && key0 + WKC - 1 > pmin) || !row_ok;
+        const int lim = (CAUSAL ? min(N - 1, qpos) : N - 1) - key0 - 4 * g;
+        floatx4 ds[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = !need_mask || (row_ok && kb * 16 + j <= lim);
+                const float pv = ok ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][j], c2, -my_lse2)) : 0.0f;
+                ds[kb][j] = pv * (dp[kb][j] - my_d);
+            }
+        const half8 sb = pack_slots(ds[0], ds[1]);
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) {
+            const int d = wave + 4 * i;
+            if (DB % 4 == 0 || d < DB) dq[i] = mfma16(tile_tr<W>(sK[cur], d * 16, g, trow, tcol), sb, dq[i]);
+        }
+        if (more) {
+            lk.store(sK[cur ^ 1]);
+            lv.store(sV[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+    if (!row_ok) return;
+    f16* qdst = p.out + ((int64_t)b * NH + myrow) * DH;
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const int d = wave + 4 * i;
+        if (DB % 4 == 0 || d < DB) {
+            const u32x2 w2 = {pack_h2(dq[i][0] * p.scale, dq[i][1] * p.scale), pack_h2(dq[i][2] * p.scale, dq[i][3] * p.scale)};
+            *reinterpret_cast<u32x2*>(qdst + d * 16 + g * 4) = w2;
+        }
+    }
+}
+
+template <int DH>
+hipError_t launch_fwd_wide(const FlashArgs& a, bool causal, hipStream_t st) {
+    dim3 grid((unsigned)((a.N * a.H + 15) / 16), (unsigned)a.B);
+    if (causal) hipLaunchKernelGGL((flash_fwd_wide<DH, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((flash_fwd_wide<DH, false>), grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// dK/dV and dQ in one launch: blocks [0, nkv) of a batch take 16 keys
+// each, the rest 16 query rows each; the two roles share nothing, so their
+// latency chains overlap on the GPU.
+template <int DH, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_bwd_wide(FlashArgs p, int nkv) {
+    __shared__ __attribute__((aligned(16))) char lds[bwd_wide_lds<DH>()];
+    if ((int)blockIdx.x < nkv) bwd_dkdv_wide<DH, CAUSAL>(p, blockIdx.x, lds);
+    else bwd_dq_wide<DH, CAUSAL>(p, blockIdx.x - nkv, lds);
+}
+
+template <int DH>
+hipError_t launch_bwd_wide(const FlashArgs& a, bool causal, hipStream_t st) {
+    const int nkv = (a.N + 15) / 16, nq = (a.N * a.H + 15) / 16;
+    dim3 grid((unsigned)(nkv + nq), (unsigned)a.B);
+    if (causal) hipLaunchKernelGGL((flash_bwd_wide<DH, true>), grid, dim3(256), 0, st, a, nkv);
+    else hipLaunchKernelGGL((flash_bwd_wide<DH, false>), grid, dim3(256), 0, st, a, nkv);
+    return hipGetLastError();
+}
+
+// Head sizes with wide kernels (multiples of 16 up to 256 not covered by
+// the specialised kernels): calls f.template operator()<DH>().
+template <class F>
+hipError_t wide_dispatch(int dh, F&& f) {
+    switch (dh) {
+        case 16: return f(std::integral_constant<int, 16>{});
+        case 48: return f(std::integral_constant<int, 48>{});
+        case 80: return f(std::integral_constant<int, 80>{});
+        case 96: return f(std::integral_constant<int, 96>{});
+        case 112: return f(std::integral_constant<int, 112>{});
+        case 144: return f(std::integral_constant<int, 144>{});
+        case 160: return f(std::integral_constant<int, 160>{});
+        case 176: return f(std::integral_constant<int, 176>{});
+        case 192: return f(std::integral_constant<int, 192>{});
+        case 208: return f(std::integral_constant<int, 208>{});
+        case 224: return f(std::integral_constant<int, 224>{});
+        case 240: return f(std::integral_constant<int, 240>{});
+        case 256: return f(std::integral_constant<int, 256>{});
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool flash_wide_head(uint32_t dh) {
+    return dh % 16 == 0 && dh >= 16 && dh <= 256 && dh != 32 && dh != 64 && dh != 128;
+}
+
+hipError_t flash_forward_wide(const FlashArgs& a, int dh, bool causal, hipStream_t st) {
+    return wide_dispatch(dh, [&](auto D) { return launch_fwd_wide<decltype(D)::value>(a, causal, st); });
+}
+
+hipError_t flash_backward_wide(const FlashArgs& a, int dh, bool causal, hipStream_t st) {
+    return wide_dispatch(dh, [&](auto D) { return launch_bwd_wide<decltype(D)::value>(a, causal, st); });
+}
+
+}  // namespace evkhip

@@ -47,8 +47,14 @@ struct FlashArgs {
     float scale;
     int spin_limit;    // iterations of a bounded in-kernel wait before it gives up
 };
+// flash_wide.hip: MFMA forward / backward for the other multiples of 16 up
+// to 256.  The backward takes the forward's O and LSE in a.o / a.lse (no
+// workspace).
+bool flash_wide_head(uint32_t dh);
+hipError_t flash_forward_wide(const FlashArgs& a, int dh, bool causal, hipStream_t st);
+hipError_t flash_backward_wide(const FlashArgs& a, int dh, bool causal, hipStream_t st);
 // Head sizes with MFMA forward and backward kernels.
-inline bool flash_mfma_head(uint32_t dh) { return dh == 32 || dh == 64 || dh == 128; }
+inline bool flash_mfma_head(uint32_t dh) { return dh == 32 || dh == 64 || dh == 128 || flash_wide_head(dh); }
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 void flash_free_workspace();

@@ -90,7 +90,7 @@ int evkhip_fill(void* data, uint64_t bytes, uint32_t pattern, void* stream) {
     return EVKHIP_OK;
 }
 int evkhip_flash_has_mfma(uint32_t head_dim) {
-    return head_dim == 32 || head_dim == 64 || head_dim == 128;
+    return head_dim % 16 == 0 && head_dim >= 16 && head_dim <= 256;
 }
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
                            const evkhip_tensor* o, int causal, float* lse, void* stream) {

@@ -316,13 +316,20 @@ static void test_training_host() {
     gu.eval(false);
     const std::vector<std::string> unfused = {"matmul", "apply_causal_mask", "softmax", "matmul"};
     TEST(ops_of_log() == unfused);
-    // a head size without MFMA flash kernels keeps the unfused chain
+    // a head size without MFMA flash kernels keeps the unfused chain; the
+    // reference's own head of 256 takes the fused one
     Graph gd;
-    Tensor& q3 = gd.tensor({2, 16, 48}, true);
+    Tensor& q3 = gd.tensor({2, 16, 40}, true);
     gd.causal_attention(q3, q3, q3);
     stub_clear_log();
     gd.eval(false);
-    TEST(!evkhip_flash_has_mfma(48) && ops_of_log() == unfused);
+    TEST(!evkhip_flash_has_mfma(40) && ops_of_log() == unfused);
+    Graph gw;
+    Tensor& q4 = gw.tensor({2, 16, 256}, true);
+    gw.causal_attention(q4, q4, q4);
+    stub_clear_log();
+    gw.eval(false);
+    TEST(evkhip_flash_has_mfma(256) && ops_of_log() == std::vector<std::string>{"flash_attention"});
     evk::ai::SubmitCmd(true);
     TEST(mock_errors() == 0);
 }

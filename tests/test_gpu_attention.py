@@ -125,7 +125,7 @@ def test_config3_causal_flash_backward(dev, orc, use_lse):
     assert_close_f16(dv, wv, what="dV")
 
 
-@pytest.mark.parametrize("Dh", [32, 64, 128, 16, 256])
+@pytest.mark.parametrize("Dh", [32, 64, 128, 16, 48, 96, 256])
 @pytest.mark.parametrize("N", [16, 45, 96])
 def test_flash_backward_ragged(dev, orc, Dh, N):
     import evk_amd as evk
@@ -316,3 +316,30 @@ def test_kv_cache_write(dev, orc):
         want = cache.copy()
         want[:, pos0:pos0 + n] = src
         assert np.array_equal(from_dev(C), want)
+
+
+@pytest.mark.parametrize("use_lse", [True, False])
+def test_reference_training_shape_d256(dev, orc, use_lse):
+    """The shape the reference trains with: Graph::causal_attention over one
+    head of 256 for B=16 sequences of 160 (example/main_llm.cpp:694-702,
+    evk_ai.h:961-1007), forward and backward on the MFMA head-256 kernels,
+    against the oracle; plus the row-sum invariant with V = 1."""
+    import evk_amd as evk
+    assert evk.lib().evkhip_flash_has_mfma(256) == 1
+    B, N, D = 16, 160, 256
+    q = orc.normal_f16((B, N, D), 281)
+    k = orc.normal_f16((B, N, D), 282)
+    v = orc.normal_f16((B, N, D), 283)
+    g = orc.normal_f16((B, N, D), 284)
+    o, lse = fwd(evk, dev, q, k, v, True)
+    wo, wl = orc.attention_fwd(q, k, v, True)
+    assert_close_f16(o, wo, what="O d256")
+    assert np.abs(lse - wl).max() < 1e-2
+    dq, dk, dv = bwd(evk, dev, q, k, v, g, True, use_lse)
+    wq, wk, wv = orc.attention_bwd(q, k, v, g, True)
+    assert_close_f16(dq, wq, what="dQ d256")
+    assert_close_f16(dk, wk, what="dK d256")
+    assert_close_f16(dv, wv, what="dV d256")
+    ones = np.full((B, N, D), f16(1.0), np.uint16)
+    o1, _ = fwd(evk, dev, q, k, ones, True)
+    assert np.abs(f32(o1) - 1.0).max() <= 1e-3
