@@ -509,6 +509,30 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         buf_rsrc(p.q + ((int64_t)b * NH + R0) * DH, (uint32_t)(last - R0 + 1) * DH * 2);
     f16* vslot = vslot_all + wave * L::VSLOT;
 
+    // chunk registers: K A-operands (key 16 kb + l16, dh 32 ks + 8 g) and this
+    // lane's V pieces (16 bytes at byte lane*16 + i*1024 of the chunk).  Each
+    // chunk gets descriptors over its own keys [c*KC, N), so keys past N read
+    // as zeros.
+    const uint32_t k_vo = (uint32_t)(l16 * DH + g * 8) * 2;
+    const uint32_t v_vo = (uint32_t)lane * 16;
+    u32x4 kr[2][KS], vr[VPER];
+    auto load_chunk = [&](int c) {
+        const uint32_t rem = (uint32_t)(N - c * KC) * DH * 2;
+        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (int64_t)c * KC * DH, rem);
+        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (int64_t)c * KC * DH, rem);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, 0);
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, 0);
+    };
+
+    // the first chunk's loads go out before the Q tile's staging: K and V do
+    // not depend on Q, so the two memory latencies overlap
+    int c = wave;
+    if (c < nch) load_chunk(c);
+
     // Q^T B operands: query R0 + 16 qb + l16, dh [32 ks + 8 g, +8)
     // the tile's Q goes through LDS once (each wave of the half loads a
     // quarter), then every wave reads its fragments from there
@@ -548,27 +572,6 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f,
                          (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
 
-    // chunk registers: K A-operands (key 16 kb + l16, dh 32 ks + 8 g) and this
-    // lane's V pieces (16 bytes at byte lane*16 + i*1024 of the chunk).  Each
-    // chunk gets descriptors over its own keys [c*KC, N), so keys past N read
-    // as zeros.
-    const uint32_t k_vo = (uint32_t)(l16 * DH + g * 8) * 2;
-    const uint32_t v_vo = (uint32_t)lane * 16;
-    u32x4 kr[2][KS], vr[VPER];
-    auto load_chunk = [&](int c) {
-        const uint32_t rem = (uint32_t)(N - c * KC) * DH * 2;
-        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (int64_t)c * KC * DH, rem);
-        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (int64_t)c * KC * DH, rem);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, 0);
-#pragma unroll
-        for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, 0);
-    };
-
-    int c = wave;
-    if (c < nch) load_chunk(c);
     const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
     // chunks below cu need no mask (all keys in range and, causal, at or
     // before every row's position); the masked tail runs a separate body so

@@ -157,6 +157,13 @@ __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
     const __amdgpu_buffer_rsrc_t vres = buf_rsrc(p.v + (int64_t)b * N * DH, (uint32_t)N * DH * 2u);
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
 
+    // the first tile's loads go out first (they do not depend on Q), then Q
+    WideTile<DH> lk, lv;
+    const int nkt = (kend + WKC - 1) / WKC;
+    if (nkt > 0) {
+        lk.load(kres, 0);
+        lv.load(vres, 0);
+    }
     half4 qf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = ld_h4(qres, row_ok, myrow * DH + ks * 16 + g * 4);
@@ -171,11 +178,7 @@ __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
     float m_ref = -INFINITY;
     const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
 
-    WideTile<DH> lk, lv;
-    const int nkt = (kend + WKC - 1) / WKC;
     if (nkt > 0) {
-        lk.load(kres, 0);
-        lv.load(vres, 0);
         lk.store(sK[0]);
         lv.store(sV[0]);
     }
@@ -321,7 +324,6 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
         kf[ks] = ld_h4(kres, key_ok, mykey * DH + ks * 16 + g * 4);
         vf[ks] = ld_h4(vres, key_ok, mykey * DH + ks * 16 + g * 4);
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): see flash_fwd_wide
     floatx4 dk[DPW], dv[DPW];
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
@@ -351,6 +353,12 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
         lq.load(qres, rstart);
         lg.load(gres, rstart);
         load_stats(0);
+    }
+    // drain the key operands' and the first tile's loads together: inside
+    // the loop only the next tile's loads are then in flight (see
+    // flash_fwd_wide)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if (nrt > 0) {
         lq.store(sQ[0]);
         lg.store(sG[0]);
         store_stats(0);
@@ -445,6 +453,12 @@ __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
     const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
     const float my_lse2 = row_ok ? p.lse[((int64_t)b * H + myrow % H) * N + qpos] * kLog2e : 0.0f;
 
+    WideTile<DH> lk, lv;
+    const int nkt = (kend + WKC - 1) / WKC;
+    if (nkt > 0) {  // before the row operands: they do not depend on each other
+        lk.load(kres, 0);
+        lv.load(vres, 0);
+    }
     half4 qf[KS], gf[KS];
     float my_d = 0.0f;  // D = rowsum(dO * O): this lane's dh, then the row's four lane groups
 #pragma unroll
@@ -462,11 +476,7 @@ __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
 #pragma unroll
     for (int i = 0; i < DPW; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    WideTile<DH> lk, lv;
-    const int nkt = (kend + WKC - 1) / WKC;
     if (nkt > 0) {
-        lk.load(kres, 0);
-        lv.load(vres, 0);
         lk.store(sK[0]);
         lv.store(sV[0]);
     }
