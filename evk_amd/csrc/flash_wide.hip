@@ -9,8 +9,11 @@
 // position r/H of head r%H.
 //
 // MFMA forms (lane l, g = l/16, l16 = l%16):
-//   v_mfma_f32_16x16x16_f16 for contractions over Dh (16 per step):
-//       A row l16, B column l16, k = 4g..4g+3; D column l16, rows 4g+j.
+//   contractions over Dh: v_mfma_f32_16x16x32_f16 per 32 dims (A row l16,
+//       B column l16, k = 8g..8g+7 of the step; the A fragment is one
+//       16-byte LDS read), and for Dh an odd multiple of 16 one
+//       v_mfma_f32_16x16x16_f16 for the last 16 (k = 4g..4g+3); D column
+//       l16, rows 4g+j.
 //   v_mfma_f32_16x16x32_f16 for contractions over 32 keys or 32 rows:
 //       operand slot s of lane l holds k = 4g+s (s < 4) or 16+4g+s-4, which
 //       is exactly how two 16-wide D blocks lay out their rows, so
@@ -82,39 +85,61 @@ DEV half8 tile_tr(const f16* t, int c0, int g, int trow, int tcol) {
     return cat4(lds_read_tr(base), lds_read_tr(base + 16 * W));
 }
 
-// NT independent 16 x 16 blocks of D = A B^T contracted over DH (16x16x16
-// steps): block t takes A rows r0[t] + l16 of LDS tile a[t] (rows of W
-// halves) and the B fragments bf[t] from registers; D element j: row
-// r0[t] + 4 g + j, column l16.  The blocks advance together (independent
-// accumulators keep the MFMA pipe busy) and the A fragments of step ks + 1
-// are requested before the MFMAs of step ks.
-template <int DH, int W, int NT>
-DEV void contract_dh(const f16* const (&a)[NT], const int (&r0)[NT], const half4* const (&bf)[NT], int l16, int g,
-                     floatx4 (&acc)[NT]) {
-    constexpr int KS = DH / 16;
-    const f16* row[NT];
+// One row of DH halves (a query, key or dO row) as B fragments of the Dh
+// contraction: m[ks] holds dims 32 ks + 8 g .. +7, t the tail dims
+// 32 K32 + 4 g .. +3 when DH is an odd multiple of 16.
+template <int DH>
+struct RowFrag {
+    static constexpr int K32 = DH / 32;
+    static constexpr bool TAIL = DH % 32 != 0;
+    half8 m[K32 > 0 ? K32 : 1];
+    half4 t;
+    DEV void load(__amdgpu_buffer_rsrc_t res, bool ok, int row, int g) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        row[t] = a[t] + (r0[t] + l16) * W + g * 4;
-        acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < K32; ++ks)
+            m[ks] = as_half8(buf_load16(res, oob_or(ok, (uint32_t)(row * DH + 32 * ks + 8 * g) * 2u), 0));
+        if (TAIL) t = ld_h4(res, ok, row * DH + 32 * K32 + 4 * g);
     }
-    half4 cur[NT], nxt[NT];
+};
+
+// One 16 x 16 block of D = A B^T contracted over the 32-wide steps
+// [S0, S1) of DH, plus the 16-wide tail when TAIL: A rows r0 + l16 of the
+// LDS tile a (rows of W halves; W * 2 bytes is an odd multiple of 16, so
+// the 16 rows of a 16-byte read hit distinct banks), B fragments bf; D
+// element j: row r0 + 4 g + j, column l16.  Every A fragment is requested
+// before the first MFMA.
+template <int DH, int W, int S0, int S1, bool TAIL>
+DEV floatx4 contract_steps(const f16* a, int r0, const RowFrag<DH>& bf, int l16, int g) {
+    const f16* row = a + (r0 + l16) * W;
+    half8 fr[S1 > S0 ? S1 - S0 : 1];
+    half4 tl;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) cur[t] = *reinterpret_cast<const half4*>(row[t]);
+    for (int ks = S0; ks < S1; ++ks) fr[ks - S0] = *reinterpret_cast<const half8*>(row + 32 * ks + 8 * g);
+    if (TAIL) tl = *reinterpret_cast<const half4*>(row + 32 * RowFrag<DH>::K32 + 4 * g);
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) nxt[t] = *reinterpret_cast<const half4*>(row[t] + (ks + 1) * 16);
-        }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = mfma_k16(cur[t], bf[t][ks], acc[t]);
-        if (ks + 1 < KS) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) cur[t] = nxt[t];
-        }
+    for (int ks = S0; ks < S1; ++ks) acc = mfma16(fr[ks - S0], bf.m[ks], acc);
+    if (TAIL) {
+        // the tail goes to an accumulator of its own: a 16x16x16 MFMA that
+        // takes a 16x16x32 MFMA's result as its C operand right behind it
+        // read wrong values on MI355X
+        const floatx4 t = mfma_k16(tl, bf.t, floatx4{0.f, 0.f, 0.f, 0.f});
+        acc = (S1 > S0) ? acc + t : t;
     }
+    return acc;
 }
+template <int DH, int W>
+DEV floatx4 contract_full(const f16* a, int r0, const RowFrag<DH>& bf, int l16, int g) {
+    return contract_steps<DH, W, 0, RowFrag<DH>::K32, RowFrag<DH>::TAIL>(a, r0, bf, l16, g);
+}
+
+// The four waves of a workgroup hand 16 x 16 fp32 blocks to each other
+// through LDS: wave w writes its block at x + 64 w lanes (16 bytes a lane,
+// the same lane-to-element map in every wave), and after a barrier any wave
+// reads block w' at the same lane.
+DEV void xput(floatx4* x, int wave, int lane, const floatx4& v) { x[wave * 64 + lane] = v; }
+DEV floatx4 xget(const floatx4* x, int w, int lane) { return x[w * 64 + lane]; }
+constexpr int XBYTES = 4 * 64 * 16;
 
 // dh blocks (16 wide) of a wave when four waves share DB of them
 template <int DB>
@@ -126,10 +151,11 @@ struct DhShare {
 // Forward: O and the public LSE.  Grid (ceil(N*H/16), B), 4 waves per
 // workgroup for 16 query rows R0 + l16 (the B operand Q^T in registers).
 // K and V come in 32-key tiles staged in LDS for the workgroup (double
-// buffered).  Every wave forms the tile's scores and probabilities itself
-// (a 32 x 16 block, cheap next to loading the tile), and wave w multiplies
-// them into dh blocks w, w+4, ... of the output:
-//   S^T(16 keys x 16 q) = K Q^T   (DH/16 steps of 16x16x16)
+// buffered).  The tile's scores are two 16 x 16 blocks (keys 0-15, 16-31);
+// wave w contracts block w % 2 over one half of Dh (w / 2), the four parts
+// go through LDS, and every wave adds them up and forms the probabilities
+// itself, then multiplies them into dh blocks w, w+4, ... of the output:
+//   S^T(16 keys x 16 q) = K Q^T   (contraction over Dh, split in halves)
 //   O^T(16 dh x 16 q) += V^T P^T  (16x16x32, V^T by tr reads)
 //   row sums: ones . P^T on the MFMA.
 // Rescaling is lazy: a row's reference maximum moves only when a chunk has a
@@ -137,14 +163,16 @@ struct DhShare {
 // ---------------------------------------------------------------------------
 template <int DH, bool CAUSAL>
 __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
-    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    constexpr int DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
     __shared__ __attribute__((aligned(16))) f16 sK[2][WKC * W];
     __shared__ __attribute__((aligned(16))) f16 sV[2][WKC * W];
+    __shared__ floatx4 sX[4 * 64];
 
     const int H = p.H, N = p.N, NH = N * H;
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4, trow = l16 >> 2, tcol = (l16 & 3) * 4;
+    constexpr int K32 = RowFrag<DH>::K32, HS = (K32 + 1) / 2;  // the first half: steps [0, HS)
     const int R0 = blockIdx.x * 16;
     const int myrow = R0 + l16;
     const bool row_ok = myrow < NH;
@@ -164,9 +192,8 @@ __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
         lk.load(kres, 0);
         lv.load(vres, 0);
     }
-    half4 qf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = ld_h4(qres, row_ok, myrow * DH + ks * 16 + g * 4);
+    RowFrag<DH> qf;
+    qf.load(qres, row_ok, myrow, g);
     // drain these loads here: inside the loop the only loads in flight are
     // then the next tile's, which the loop waits for at its LDS store only
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -192,8 +219,15 @@ __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
         }
         const int key0 = kt * WKC;
         // element j of s[kb]: key key0 + 16 kb + 4 g + j, query myrow
+        {
+            const floatx4 part = (wave & 2) ? contract_steps<DH, W, HS, K32, RowFrag<DH>::TAIL>(sK[cur], 16 * (wave & 1), qf, l16, g)
+                                            : contract_steps<DH, W, 0, HS, false>(sK[cur], 16 * (wave & 1), qf, l16, g);
+            xput(sX, wave, lane, part);
+        }
+        __syncthreads();
         floatx4 s[2];
-        contract_dh<DH, W, 2>({sK[cur], sK[cur]}, {0, 16}, {qf, qf}, l16, g, s);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) s[kb] = xget(sX, kb, lane) + xget(sX, kb + 2, lane);
         if ((key0 + WKC > N) || (CAUSAL && key0 + WKC - 1 > pmin)) {
             const int lim = (CAUSAL ? min(N - 1, qpos) : N - 1) - key0 - 4 * g;
 #pragma unroll
@@ -252,55 +286,40 @@ __global__ __launch_bounds__(256) void flash_fwd_wide(FlashArgs p) {
 // (K^T, V^T as B-operand registers) and walks every query row at or after
 // k0 in 32-row tiles of Q and dO (with their lse2 and D) staged in LDS for
 // the workgroup, so the MQA sum over heads happens in the accumulation.
-// Every wave forms the tile's P and dS itself; wave w accumulates dh blocks
+// The tile's S and dP are four 16 x 16 blocks (rows 0-15, 16-31 of each);
+// wave w contracts block w and hands it to the others through LDS.  Every
+// wave forms the tile's P and dS itself; wave w accumulates dh blocks
 // w, w+4, ... of dK and dV:
-//   S, dP (16 rows x 16 keys) = Q K^T, dO V^T  (16x16x16 over DH)
+//   S, dP (16 rows x 16 keys) = Q K^T, dO V^T  (contractions over DH)
 //   P = 2^(S c - lse2_row), dS = P (dP - D_row)
 //   dV^T(16 dh x 16 keys) += dO^T P, dK^T += Q^T dS  (16x16x32 over rows)
 // ---------------------------------------------------------------------------
-// D = rowsum(dO * O) of a 32-row tile, any DH (a multiple of 16): thread t
-// takes row t / 8 and the half pairs 2 (t % 8) + 16 m of it (4-byte loads),
-// the 8 threads of a row (consecutive lanes) add up with shuffles.
-template <int DH>
-struct RowDot {
-    uint32_t o[DH / 16], g[DH / 16];
-    DEV void load(__amdgpu_buffer_rsrc_t ores, __amdgpu_buffer_rsrc_t gres, int row0, int nrows) {
-        const int row = row0 + (int)(threadIdx.x >> 3), c = 2 * (int)(threadIdx.x & 7);
+// Dot product of two 16-byte pieces (8 halves each), in fp32.
+DEV float dot8(const u32x4& a, const u32x4& b) {
+    const half8 x = as_half8(a), y = as_half8(b);
+    float acc = 0.0f;
 #pragma unroll
-        for (int m = 0; m < DH / 16; ++m) {
-            const uint32_t off = oob_or(row < nrows, (uint32_t)(row * DH + c + 16 * m) * 2u);
-            o[m] = __builtin_amdgcn_raw_buffer_load_b32(ores, off, 0, 0);
-            g[m] = __builtin_amdgcn_raw_buffer_load_b32(gres, off, 0, 0);
-        }
-    }
-    // the sum, in every lane of the row's eight
-    DEV float sum() const {
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < DH / 16; ++m) {
-            const half2_t a = __builtin_bit_cast(half2_t, o[m]), b = __builtin_bit_cast(half2_t, g[m]);
-            acc = __builtin_fmaf((float)a[0], (float)b[0], acc);
-            acc = __builtin_fmaf((float)a[1], (float)b[1], acc);
-        }
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 4, 64);
-        return acc;
-    }
-};
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)x[e], (float)y[e], acc);
+    return acc;
+}
 
 // LDS of a flash_bwd_wide workgroup, either role: two double-buffered
-// 32-row tiles, then (dK/dV) the tiles' lse2 and D
+// 32-row tiles, then (dK/dV) the tiles' lse2 and D, the block exchange and
+// the per-piece dO . O products of the next tile
 template <int DH>
-constexpr int bwd_wide_lds() { return 2 * 2 * WKC * WideTile<DH>::W * 2 + 2 * 2 * WKC * 4; }
+constexpr int bwd_wide_lds() {
+    return 2 * 2 * WKC * WideTile<DH>::W * 2 + 2 * 2 * WKC * 4 + XBYTES + WideTile<DH>::PIECES * 4;
+}
 
 template <int DH, bool CAUSAL>
 __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
-    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    constexpr int DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
     f16 (*sQ)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds);
     f16 (*sG)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds + 2 * WKC * W * 2);
     float (*sL)[WKC] = reinterpret_cast<float (*)[WKC]>(lds + 4 * WKC * W * 2);
     float (*sD)[WKC] = reinterpret_cast<float (*)[WKC]>(lds + 4 * WKC * W * 2 + 2 * WKC * 4);
+    floatx4* sX = reinterpret_cast<floatx4*>(lds + 4 * WKC * W * 2 + 4 * WKC * 4);
+    float* sPart = reinterpret_cast<float*>(lds + 4 * WKC * W * 2 + 4 * WKC * 4 + XBYTES);
 
     const int H = p.H, N = p.N, NH = N * H;
     const int b = blockIdx.y;
@@ -316,14 +335,11 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
     const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
-    const float* lse_b = p.lse + (int64_t)b * H * N;
+    const __amdgpu_buffer_rsrc_t lres = buf_rsrc(p.lse + (int64_t)b * H * N, (uint32_t)(H * N) * 4u);
 
-    half4 kf[KS], vf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        kf[ks] = ld_h4(kres, key_ok, mykey * DH + ks * 16 + g * 4);
-        vf[ks] = ld_h4(vres, key_ok, mykey * DH + ks * 16 + g * 4);
-    }
+    RowFrag<DH> kf, vf;
+    kf.load(kres, key_ok, mykey, g);
+    vf.load(vres, key_ok, mykey, g);
     floatx4 dk[DPW], dv[DPW];
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
@@ -334,49 +350,61 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
     // rows of positions >= k0 (causal), in tiles of 32
     const int rstart = CAUSAL ? min(NH, k0 * H) / WKC * WKC : 0;
     const int nrt = (NH - rstart + WKC - 1) / WKC;
-    // per row of a tile: lse2 = LSE * log2(e) of (position, head), and D
-    WideTile<DH> lq, lg;
-    RowDot<DH> rd;
+    // per row of a tile: lse2 = LSE * log2(e) of (position, head), and
+    // D = rowsum(dO * O).  The LSE is loaded as it is and scaled when it goes
+    // to LDS: arithmetic on it at the load would make the wave wait there for
+    // every load in flight, the next tile's included.  O comes in the dO
+    // tile's piece layout; each thread stores the dot products of its pieces
+    // and, after the next barrier, the first WKC threads add their row's
+    // DH / 8 products in order.
+    constexpr int PPR = DH / 8;  // pieces per row
+    WideTile<DH> lq, lg, lo;
     float lsv = 0.0f;
-    auto load_stats = [&](int t) {
+    auto load_tile = [&](int t) {
         const int r0 = rstart + t * WKC;
-        rd.load(ores, gres, r0, NH);
+        lq.load(qres, r0);
+        lg.load(gres, r0);
+        lo.load(ores, r0);
         const int r = r0 + (int)threadIdx.x;
-        lsv = (threadIdx.x < WKC && r < NH) ? lse_b[(r % H) * N + r / H] * kLog2e : 0.0f;
+        lsv = buf_load_f32(lres, oob_or(threadIdx.x < WKC && r < NH, (uint32_t)((r % H) * N + r / H) * 4u));
     };
-    auto store_stats = [&](int st) {
-        const float d = rd.sum();
-        if ((threadIdx.x & 7) == 0) sD[st][threadIdx.x >> 3] = d;
-        if (threadIdx.x < WKC) sL[st][threadIdx.x] = lsv;
+    auto stage_tile = [&](int st) {
+        lq.store(sQ[st]);
+        lg.store(sG[st]);
+#pragma unroll
+        for (int i = 0; i < WideTile<DH>::PER; ++i) {
+            const int pc = threadIdx.x + 256 * i;
+            if (WideTile<DH>::PIECES % 256 == 0 || pc < WideTile<DH>::PIECES) sPart[pc] = dot8(lg.r[i], lo.r[i]);
+        }
+        if (threadIdx.x < WKC) sL[st][threadIdx.x] = lsv * kLog2e;
     };
-    if (nrt > 0) {
-        lq.load(qres, rstart);
-        lg.load(gres, rstart);
-        load_stats(0);
-    }
+    auto finish_d = [&](int st) {
+        if (threadIdx.x < WKC) {
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < PPR; ++c) d += sPart[threadIdx.x * PPR + c];
+            sD[st][threadIdx.x] = d;
+        }
+    };
+    if (nrt > 0) load_tile(0);
     // drain the key operands' and the first tile's loads together: inside
     // the loop only the next tile's loads are then in flight (see
     // flash_fwd_wide)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    if (nrt > 0) {
-        lq.store(sQ[0]);
-        lg.store(sG[0]);
-        store_stats(0);
-    }
+    if (nrt > 0) stage_tile(0);
     __syncthreads();
     for (int rt = 0; rt < nrt; ++rt) {
         const int cur = rt & 1;
         const bool more = rt + 1 < nrt;
-        if (more) {
-            lq.load(qres, rstart + (rt + 1) * WKC);
-            lg.load(gres, rstart + (rt + 1) * WKC);
-            load_stats(rt + 1);
-        }
+        if (more) load_tile(rt + 1);
+        finish_d(cur);
         const int r0 = rstart + rt * WKC;
         // element j of s[rb]: row r0 + 16 rb + 4 g + j, key mykey
-        floatx4 sd[4];  // S rows 0-15, 16-31, then dP
-        contract_dh<DH, W, 4>({sQ[cur], sQ[cur], sG[cur], sG[cur]}, {0, 16, 0, 16}, {kf, kf, vf, vf}, l16, g, sd);
-        const floatx4 s[2] = {sd[0], sd[1]}, dp[2] = {sd[2], sd[3]};
+        // wave w: block w of S rows 0-15, 16-31, then dP rows 0-15, 16-31
+        xput(sX, wave, lane, contract_full<DH, W>((wave & 2) ? sG[cur] : sQ[cur], 16 * (wave & 1),
+                                                  (wave & 2) ? vf : kf, l16, g));
+        __syncthreads();
+        const floatx4 s[2] = {xget(sX, 0, lane), xget(sX, 1, lane)}, dp[2] = {xget(sX, 2, lane), xget(sX, 3, lane)};
         floatx4 pe[2], ds[2];
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -397,11 +425,7 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
                 dk[i] = mfma16(tile_tr<W>(sQ[cur], d * 16, g, trow, tcol), sb, dk[i]);
             }
         }
-        if (more) {
-            lq.store(sQ[cur ^ 1]);
-            lg.store(sG[cur ^ 1]);
-            store_stats(cur ^ 1);
-        }
+        if (more) stage_tile(cur ^ 1);
         __syncthreads();
     }
     if (!key_ok) return;
@@ -422,17 +446,20 @@ __device__ void bwd_dkdv_wide(const FlashArgs& p, int bx, char* lds) {
 
 // ---------------------------------------------------------------------------
 // dQ (blocks of flash_bwd_wide).  4 waves for 16 query rows (Q^T and dO^T as B
-// operands); K and V in 32-key tiles staged in LDS as in the forward; every
-// wave forms dS, wave w accumulates dh blocks w, w+4, ... of dQ:
-//   S^T, dP^T (16 keys x 16 q) = K Q^T, V dO^T  (16x16x16 over DH)
+// operands); K and V in 32-key tiles staged in LDS as in the forward; the
+// tile's S^T and dP^T are four 16 x 16 blocks, one per wave, handed over
+// through LDS; every wave forms dS, wave w accumulates dh blocks w, w+4,
+// ... of dQ:
+//   S^T, dP^T (16 keys x 16 q) = K Q^T, V dO^T  (contractions over DH)
 //   dS^T = P^T (dP^T - D), P = 2^(S c - lse2_row)
 //   dQ^T(16 dh x 16 q) += K^T dS^T  (16x16x32 over keys, K^T by tr reads)
 // ---------------------------------------------------------------------------
 template <int DH, bool CAUSAL>
 __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
-    constexpr int KS = DH / 16, DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
+    constexpr int DB = DH / 16, DPW = DhShare<DB>::PER, W = WideTile<DH>::W;
     f16 (*sK)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds);
     f16 (*sV)[WKC * W] = reinterpret_cast<f16 (*)[WKC * W]>(lds + 2 * WKC * W * 2);
+    floatx4* sX = reinterpret_cast<floatx4*>(lds + 4 * WKC * W * 2 + 4 * WKC * 4);
 
     const int H = p.H, N = p.N, NH = N * H;
     const int b = blockIdx.y;
@@ -451,7 +478,8 @@ __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
     const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2u);
-    const float my_lse2 = row_ok ? p.lse[((int64_t)b * H + myrow % H) * N + qpos] * kLog2e : 0.0f;
+    const __amdgpu_buffer_rsrc_t lres = buf_rsrc(p.lse + (int64_t)b * H * N, (uint32_t)(H * N) * 4u);
+    const float my_lse = buf_load_f32(lres, oob_or(row_ok, (uint32_t)((myrow % H) * N + qpos) * 4u));
 
     WideTile<DH> lk, lv;
     const int nkt = (kend + WKC - 1) / WKC;
@@ -459,19 +487,23 @@ __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
         lk.load(kres, 0);
         lv.load(vres, 0);
     }
-    half4 qf[KS], gf[KS];
-    float my_d = 0.0f;  // D = rowsum(dO * O): this lane's dh, then the row's four lane groups
+    RowFrag<DH> qf, gf, of;
+    qf.load(qres, row_ok, myrow, g);
+    gf.load(gres, row_ok, myrow, g);
+    of.load(ores, row_ok, myrow, g);
+    float my_d = 0.0f;  // D = rowsum(dO * O): this lane's dims, then the row's four lane groups
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        qf[ks] = ld_h4(qres, row_ok, myrow * DH + ks * 16 + g * 4);
-        gf[ks] = ld_h4(gres, row_ok, myrow * DH + ks * 16 + g * 4);
-        const half4 of = ld_h4(ores, row_ok, myrow * DH + ks * 16 + g * 4);
+    for (int ks = 0; ks < RowFrag<DH>::K32; ++ks)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) my_d = __builtin_fmaf((float)of[e], (float)gf[ks][e], my_d);
+        for (int e = 0; e < 8; ++e) my_d = __builtin_fmaf((float)of.m[ks][e], (float)gf.m[ks][e], my_d);
+    if (RowFrag<DH>::TAIL) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) my_d = __builtin_fmaf((float)of.t[e], (float)gf.t[e], my_d);
     }
     my_d += __shfl_xor(my_d, 16, 64);
     my_d += __shfl_xor(my_d, 32, 64);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): see flash_fwd_wide
+    const float my_lse2 = my_lse * kLog2e;
     floatx4 dq[DPW];
 #pragma unroll
     for (int i = 0; i < DPW; ++i) dq[i] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -489,9 +521,11 @@ __device__ void bwd_dq_wide(const FlashArgs& p, int bx, char* lds) {
             lv.load(vres, (kt + 1) * WKC);
         }
         const int key0 = kt * WKC;
-        floatx4 sd[4];  // S^T keys 0-15, 16-31, then dP^T
-        contract_dh<DH, W, 4>({sK[cur], sK[cur], sV[cur], sV[cur]}, {0, 16, 0, 16}, {qf, qf, gf, gf}, l16, g, sd);
-        const floatx4 s[2] = {sd[0], sd[1]}, dp[2] = {sd[2], sd[3]};
+        // wave w: block w of S^T keys 0-15, 16-31, then dP^T keys 0-15, 16-31
+        xput(sX, wave, lane, contract_full<DH, W>((wave & 2) ? sV[cur] : sK[cur], 16 * (wave & 1),
+                                                  (wave & 2) ? gf : qf, l16, g));
+        __syncthreads();
+        const floatx4 s[2] = {xget(sX, 0, lane), xget(sX, 1, lane)}, dp[2] = {xget(sX, 2, lane), xget(sX, 3, lane)};
         const bool need_mask = (key0 + WKC > N) || (CAUSAL && key0 + WKC - 1 > pmin) || !row_ok;
         const int lim = (CAUSAL ? min(N - 1, qpos) : N - 1) - key0 - 4 * g;
         floatx4 ds[2];
