@@ -874,6 +874,7 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
     const __amdgpu_buffer_rsrc_t qres = buf_rsrc(p.q + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
     const __amdgpu_buffer_rsrc_t gres = buf_rsrc(p.dO + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
     const __amdgpu_buffer_rsrc_t ores = buf_rsrc(p.o + (int64_t)b * NH * DH, (uint32_t)NH * DH * 2);
+    const __amdgpu_buffer_rsrc_t lres = buf_rsrc(p.lse + (int64_t)b * H * N, (uint32_t)(H * N) * 4u);
     // A thread holds at most one dO piece (DH <= 64); with it the O piece at
     // the same place, so that D = rowsum(dO * O) comes from the DH/8 lanes
     // of a row.  Rows past NH read as zeros: D = 0, lse2 = 0 (their Q and
@@ -899,11 +900,20 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int pc = threadIdx.x + 256 * i;
-            const int which = pc / PIECES, pi = pc % PIECES;
+            // PIECES is a multiple of 64, so `which` is uniform across the
+            // wave; said explicitly, the descriptor choice stays scalar (a
+            // per-lane choice costs a loop over descriptors, after which the
+            // compiler can no longer count the loads in flight and waits for
+            // all of them, the next chunk's included, before the MFMAs)
+            const int which = __builtin_amdgcn_readfirstlane(pc / PIECES), pi = pc % PIECES;
             const uint32_t off = (row0 * DH + pi * 8) * 2;
             if (2 * PIECES % 256 == 0 || pc < 2 * PIECES) {
-                pr[i] = buf_load16(which ? gres : qres, off, 0);
-                if (which) po = buf_load16(ores, off, 0);
+                if (which) {
+                    pr[i] = buf_load16(gres, off, 0);
+                    po = buf_load16(ores, off, 0);
+                } else {
+                    pr[i] = buf_load16(qres, off, 0);
+                }
             }
         }
         for (; st_next < c; ++st_next) {
@@ -914,12 +924,12 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
                 st_pos += 1;
             }
         }
-        if (threadIdx.x < BRC) {  // LSE of row row0 + t, from the (B, H, N) LSE
-            const uint32_t row = row0 + threadIdx.x;
-            sr = row < (uint32_t)NH ? p.lse[((int64_t)b * H + st_head) * N + st_pos] : 0.0f;
-        } else if (threadIdx.x < 2 * BRC) {
-            spos = st_pos;
-        }
+        // LSE of row row0 + t (t < BRC), from the (B, H, N) LSE; every
+        // thread issues the (predicated) load and uses it below, so that no
+        // path leaves it in flight
+        sr = buf_load_f32(lres, oob_or(threadIdx.x < BRC && row0 + threadIdx.x < (uint32_t)NH,
+                                       (uint32_t)(st_head * N + st_pos) * 4u));
+        if (threadIdx.x >= BRC && threadIdx.x < 2 * BRC) spos = st_pos;
     };
     auto lstore = [&](int stage) {
         f16* cs = chunk_s + stage * L::STAGE;
@@ -927,7 +937,7 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int pc = threadIdx.x + 256 * i;
-            const int which = pc / PIECES, pi = pc % PIECES;
+            const int which = __builtin_amdgcn_readfirstlane(pc / PIECES), pi = pc % PIECES;
             if (2 * PIECES % 256 == 0 || pc < 2 * PIECES) {
                 *reinterpret_cast<u32x4*>(cs + which * L::CHUNK + (pi / (DH / 8)) * RW + (pi % (DH / 8)) * 8) = pr[i];
                 if (which) dsum = dot8(as_half8(pr[i]), as_half8(po));
@@ -942,7 +952,8 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
             if (pc >= PIECES && pc < 2 * PIECES && pi % (DH / 8) == 0)
                 stats_s[stage * L::STATS + BRC + pi / (DH / 8)] = dsum;
         }
-        if (threadIdx.x < BRC) stats_s[stage * L::STATS + threadIdx.x] = sr * kLog2e;  // base-2 LSE
+        const float l2 = sr * kLog2e;  // base-2 LSE
+        if (threadIdx.x < BRC) stats_s[stage * L::STATS + threadIdx.x] = l2;
         else if (threadIdx.x < 2 * BRC) pos_s[stage * BRC + threadIdx.x - BRC] = spos;
     };
 
@@ -950,11 +961,19 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
         gload(c_lo);
         lstore(0);
     }
+    // nothing in flight from here on (the K^T, V^T operands included): the
+    // loop's waits then cover only its own loads
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
     for (int c = c_lo; c < c_hi; ++c) {
         const int stage = (c - c_lo) & 1;
-        if (c + 1 < c_hi) gload(c + 1);
+        // the next chunk is requested and staged unconditionally (past the
+        // part's last chunk the rows are either past NH, reading zeros, or
+        // rows nothing reads, staged into the stage nothing reads): with
+        // every load of an iteration consumed in that iteration, the
+        // compiler knows no load is in flight at the loop head
+        gload(c + 1);
         const int row0 = r_lo + c * BRC;
         // rows of this chunk hold positions row0/H .. (row0+31)/H
         const bool live = !CAUSAL || (row0 + BRC - 1) / H >= k0;
@@ -1035,7 +1054,7 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
                 }
             }
         }
-        if (c + 1 < c_hi) lstore(stage ^ 1);
+        lstore(stage ^ 1);
         __syncthreads();
     }
 
