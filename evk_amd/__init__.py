@@ -20,7 +20,8 @@ __all__ = [
     "lib", "available", "matmul", "flash_attention", "flash_attention_bwd",
     "single_query_attention", "rms_norm", "rope", "gelu", "add", "embed",
     "greedy_sample", "initialize", "shutdown", "ModelCfg", "model_prefill", "model_decode",
-    "model_weight_elems", "model_cache_elems", "EvkError",
+    "model_weight_elems", "model_cache_elems", "model_packed_elems", "model_pack", "model_decode_packed",
+    "EvkError",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -106,6 +107,10 @@ SIGNATURES = {
                                        C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]),
     "evkhip_model_decode": (C.c_int, [C.POINTER(ModelCfg), C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]),
+    "evkhip_model_packed_elems": (C.c_uint64, [C.POINTER(ModelCfg)]),
+    "evkhip_model_pack": (C.c_int, [C.POINTER(ModelCfg), C.c_void_p, C.c_void_p, C.c_void_p]),
+    "evkhip_model_decode_packed": (C.c_int, [C.POINTER(ModelCfg), C.c_void_p, C.c_void_p, C.c_void_p,
+                                             C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]),
 }
 
 
@@ -406,3 +411,26 @@ def model_decode(cfg: ModelCfg, weights, cache, token_io, n_steps, pos0, logits,
                                      C.c_void_p(cache.data_ptr()), C.c_void_p(token_io.data_ptr()),
                                      int(n_steps), int(pos0), C.c_void_p(logits.data_ptr()),
                                      _stream(stream)))
+
+
+def model_packed_elems(cfg: ModelCfg) -> int:
+    return int(lib().evkhip_model_packed_elems(C.byref(cfg)))
+
+
+def model_pack(cfg: ModelCfg, weights, packed, stream=None):
+    """Writes the persistent decode's layout of `weights` into `packed`
+    (model_packed_elems(cfg) fp16 elements)."""
+    if packed.numel() < model_packed_elems(cfg):
+        raise ValueError("packed needs model_packed_elems(cfg) elements")
+    _check(lib().evkhip_model_pack(C.byref(cfg), C.c_void_p(weights.data_ptr()), C.c_void_p(packed.data_ptr()),
+                                   _stream(stream)))
+
+
+def model_decode_packed(cfg: ModelCfg, packed, cache, token_io, n_steps, pos0, logits, stream=None):
+    """model_decode over packed weights, every step in one persistent launch."""
+    if token_io.numel() < n_steps + 1:
+        raise ValueError("token_io needs n_steps+1 entries")
+    _check(lib().evkhip_model_decode_packed(C.byref(cfg), C.c_void_p(packed.data_ptr()),
+                                            C.c_void_p(cache.data_ptr()), C.c_void_p(token_io.data_ptr()),
+                                            int(n_steps), int(pos0), C.c_void_p(logits.data_ptr()),
+                                            _stream(stream)))

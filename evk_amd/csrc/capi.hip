@@ -92,13 +92,20 @@ int evkhip_shutdown(void) {
     flash_free_workspace();
     decode_ops_free_workspace();
     model_free_workspace();
+    decode_persist_free_workspace();
     train_ops_free_workspace();
     return EVKHIP_OK;
 }
 
 int evkhip_device_status(uint32_t* flags, int clear) {
     EVK_RETURN_IF(!flags, EVKHIP_ERR_INVALID_ARG, "device_status: null flags");
-    return flash_status(flags, clear != 0);
+    uint32_t f = 0, g = 0;
+    int rc = flash_status(&f, clear != 0);
+    if (rc != EVKHIP_OK) return rc;
+    rc = decode_status(&g, clear != 0);
+    if (rc != EVKHIP_OK) return rc;
+    *flags = f | g;
+    return EVKHIP_OK;
 }
 
 int evkhip_debug_set_spin_limit(uint32_t iterations) {

@@ -1823,6 +1823,8 @@ void flash_set_spin_limit(uint32_t n) {
     g_spin_limit = n == 0 ? kDefaultSpinLimit : (int)std::min<uint32_t>(n - 1, (uint32_t)INT32_MAX);
 }
 
+uint32_t flash_spin_limit() { return (uint32_t)g_spin_limit; }
+
 void flash_free_workspace() {
     if (g_bwd_ws) (void)hipFree(g_bwd_ws);
     g_bwd_ws = nullptr;

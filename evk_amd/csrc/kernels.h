@@ -58,9 +58,14 @@ inline bool flash_mfma_head(uint32_t dh) { return dh == 32 || dh == 64 || dh == 
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 void flash_free_workspace();
+
+// ---- decode_persist.hip ----
+int decode_status(uint32_t* flags, bool clear);
+void decode_persist_free_workspace();
 // Device status bits raised by the flash kernels (EVKHIP_STATUS_*): read after
 // the work has completed; `clear` resets them.
 int flash_status(uint32_t* flags, bool clear);
+uint32_t flash_spin_limit();  // rounds of a bounded in-kernel wait (evkhip_debug_set_spin_limit)
 // Spin limit of the bounded in-kernel waits (0 restores the default).
 void flash_set_spin_limit(uint32_t n);
 

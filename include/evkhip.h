@@ -314,6 +314,29 @@ int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* 
                         uint16_t* token_io, uint32_t n_steps, uint32_t pos0, void* logits,
                         void* stream);
 
+/* Persistent decode (no counterpart in the reference: the reference decodes
+ * by full recompute, example/main_llm.cpp:622-654).  evkhip_model_pack writes
+ * the decode layout of a weight blob: E as is, every matrix transposed to
+ * (out, in) (Wqkv^T (3d,d), Wo^T, W1^T (hidden,d), W2^T (d,hidden), Wout^T
+ * (vocab,d)); evkhip_model_packed_elems elements, the same count.  Pack once
+ * per weight set (and again after the weights change).
+ * evkhip_model_decode_packed then has the meaning of evkhip_model_decode but
+ * runs all n_steps in one cooperative launch whose stages hand their outputs
+ * over in device memory.  It needs d and hidden multiples of 8 (at most 8192
+ * each), dh in {16,32,64,128}, max_seq <= 8192, heads * ceil(max_seq / 128)
+ * <= 144 and no more than the workgroups it runs (one per CU), and
+ * per-workgroup weight slices that fit in LDS (d=768, hidden=3072 do); other
+ * shapes (or a GPU on which the launch cannot be resident at once) return
+ * EVKHIP_ERR_UNSUPPORTED and evkhip_model_decode serves them.  Its in-kernel waits are bounded: one that
+ * gives up raises EVKHIP_STATUS_WAIT_TIMEOUT (evkhip_device_status) and the
+ * outputs of that call are then unreliable.  Calls that overlap on one GPU
+ * race on the library's hand-over buffers. */
+uint64_t evkhip_model_packed_elems(const evkhip_model_cfg* cfg);
+int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* packed, void* stream);
+int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, void* cache,
+                               uint16_t* token_io, uint32_t n_steps, uint32_t pos0, void* logits,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -138,9 +138,10 @@ def check_ids(got_ids, want_ids, logits_want):
     return None
 
 
-def gpu_generate(evk, dev, cfg, w, prompt, steps):
+def gpu_generate(evk, dev, cfg, w, prompt, steps, packed=False):
     """Prefill the prompt, then `steps` greedy steps; returns the steps+1 ids
-    (first from the prefill), prefill logits, last logits and the cache."""
+    (first from the prefill), prefill logits, last logits and the cache.
+    packed: the steps run through model_pack + model_decode_packed."""
     import torch
     W = to_dev(w, dev)
     cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
@@ -150,7 +151,12 @@ def gpu_generate(evk, dev, cfg, w, prompt, steps):
     evk.model_prefill(cfg, W, cache, feed, 0, tok, logits)
     torch.cuda.synchronize()
     first_logits = from_dev(logits).copy()
-    evk.model_decode(cfg, W, cache, tok, steps, len(prompt), logits)
+    if packed:
+        P = torch.empty(evk.model_packed_elems(cfg), dtype=torch.float16, device=dev)
+        evk.model_pack(cfg, W, P)
+        evk.model_decode_packed(cfg, P, cache, tok, steps, len(prompt), logits)
+    else:
+        evk.model_decode(cfg, W, cache, tok, steps, len(prompt), logits)
     torch.cuda.synchronize()
     return from_dev(tok), first_logits, from_dev(logits), cache
 
@@ -209,3 +215,151 @@ def test_decode_workspace_reuse(dev, orc, dims):
         stop = check_ids(list(ids), list(want_ids), want_logits)
         if stop is None:
             assert_close_f16(last_logits, want_logits[-1], what=f"last logits {kw}")
+
+
+# ---------------------------------------------------------------------------
+# Persistent decode over packed weights (evkhip_model_pack /
+# evkhip_model_decode_packed): same parity bar as model_decode.
+# ---------------------------------------------------------------------------
+def test_model_pack_layout(dev, orc):
+    """Packed blob = E, then every matrix transposed to (out, in): bit-exact
+    against numpy's transpose of the same blob."""
+    import evk_amd as evk
+    import torch
+    kw = dict(vocab=520, d=96, heads=3, layers=2, hidden=136, max_seq=16)
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=341, std=0.1)
+    P = torch.empty(evk.model_packed_elems(cfg), dtype=torch.float16, device=dev)
+    evk.model_pack(cfg, to_dev(w, dev), P)
+    torch.cuda.synchronize()
+    got = from_dev(P)
+    V, d, hid = 520, 96, 136
+    want, o = [w[:V * d]], V * d
+    for _ in range(2):
+        for (k, n) in ((d, 3 * d), (d, d), (d, hid), (hid, d)):
+            want.append(w[o:o + k * n].reshape(k, n).T.reshape(-1))
+            o += k * n
+    want.append(w[o:o + d * V].reshape(d, V).T.reshape(-1))
+    assert np.array_equal(got, np.concatenate(want))
+
+
+@pytest.mark.parametrize("kw,steps", [
+    (dict(vocab=512, d=128, heads=2, layers=2, hidden=256, max_seq=96), 20),
+    (dict(vocab=1024, d=256, heads=4, layers=3, hidden=512, max_seq=300), 12),  # several key splits
+    (dict(vocab=256, d=64, heads=4, layers=1, hidden=96, max_seq=40), 8),       # dh 16
+])
+def test_decode_packed_small(dev, orc, kw, steps):
+    import evk_amd as evk
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=351 + kw["d"], std=0.1)
+    prompt = orc.tokens_u16(kw["max_seq"] - steps - 1, 352 + kw["d"], kw["vocab"])
+    ids, first_logits, last_logits, cache = gpu_generate(evk, dev, cfg, w, prompt, steps, packed=True)
+    want_ids, want_cache, want_logits = orc.model_generate(ocfg, w, prompt, steps, return_logits=True)
+    assert evk.device_status(clear=True) == 0
+    assert_close_f16(first_logits, want_logits[0], what="prefill logits")
+    stop = check_ids(list(ids), list(want_ids), want_logits)
+    if stop is None:
+        assert_close_f16(last_logits, want_logits[-1], what="last logits")
+        assert_close_f16(from_dev(cache), want_cache, what="kv cache")
+
+
+def test_decode_config4_packed(dev, orc):
+    """C4 through the persistent decode: 1024-token prefill, 32 greedy steps,
+    ids identical to the oracle's except at near-ties."""
+    import evk_amd as evk
+    ocfg, cfg = orc.model_cfg(), evk.model_cfg()
+    w = orc.model_weights(ocfg, seed=301, std=0.02)
+    prompt = orc.tokens_u16(1024, 302, 32000)
+    ids, first_logits, last_logits, _ = gpu_generate(evk, dev, cfg, w, prompt, 32, packed=True)
+    want_ids, _, want_logits = orc.model_generate(ocfg, w, prompt, 32, return_logits=True)
+    assert evk.device_status(clear=True) == 0
+    stop = check_ids(list(ids), list(want_ids), want_logits)
+    if stop is None:
+        assert_close_f16(last_logits, want_logits[-1], what="step-32 logits")
+
+
+def test_decode_packed_repeated_and_replayed(dev, orc):
+    """The same steps three times in a row (each launch takes new hand-over
+    tags from the device), then captured into a HIP graph and replayed twice
+    with eager launches in between: identical ids and logits every time."""
+    import evk_amd as evk
+    import torch
+    kw = dict(vocab=512, d=128, heads=2, layers=2, hidden=256, max_seq=64)
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=361, std=0.1)
+    prompt = orc.tokens_u16(40, 362, 512)
+    W = to_dev(w, dev)
+    cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
+    tok = torch.zeros(9, dtype=torch.int16, device=dev)
+    logits = torch.empty(cfg.vocab, dtype=torch.float16, device=dev)
+    evk.model_prefill(cfg, W, cache, torch.from_numpy(prompt.view(np.int16)).to(dev), 0, tok, logits)
+    P = torch.empty(evk.model_packed_elems(cfg), dtype=torch.float16, device=dev)
+    evk.model_pack(cfg, W, P)
+    torch.cuda.synchronize()
+    first = tok[0].clone()
+
+    def run():
+        tok[0] = first
+        evk.model_decode_packed(cfg, P, cache, tok, 8, 40, logits)
+
+    run()
+    torch.cuda.synchronize()
+    want_tok, want_lg = tok.clone(), logits.clone()
+    for _ in range(2):
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(tok, want_tok) and torch.equal(logits, want_lg)
+    g = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(g):
+            run()
+    except Exception as ex:  # cooperative launches not capturable here
+        pytest.skip(f"graph capture of the cooperative launch failed: {ex}")
+    for _ in range(2):
+        tok.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(tok, want_tok) and torch.equal(logits, want_lg)
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(tok, want_tok) and torch.equal(logits, want_lg)
+    assert evk.device_status(clear=True) == 0
+
+
+def test_decode_packed_wait_timeout_is_reported(dev, orc):
+    """A spin limit of one round (set from the host) makes the persistent
+    decode's hand-over waits give up: every workgroup leaves, the call's
+    status raises EVKHIP_STATUS_WAIT_TIMEOUT, and the next call with the
+    default limit is correct again (it takes new tags)."""
+    import evk_amd as evk
+    import torch
+    kw = dict(vocab=512, d=128, heads=2, layers=2, hidden=256, max_seq=64)
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=371, std=0.1)
+    prompt = orc.tokens_u16(40, 372, 512)
+    want_ids, _, want_logits = orc.model_generate(ocfg, w, prompt, 6, return_logits=True)
+    W = to_dev(w, dev)
+    cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
+    tok = torch.zeros(7, dtype=torch.int16, device=dev)
+    logits = torch.empty(cfg.vocab, dtype=torch.float16, device=dev)
+    evk.model_prefill(cfg, W, cache, torch.from_numpy(prompt.view(np.int16)).to(dev), 0, tok, logits)
+    P = torch.empty(evk.model_packed_elems(cfg), dtype=torch.float16, device=dev)
+    evk.model_pack(cfg, W, P)
+    torch.cuda.synchronize()
+    first = tok[0].clone()
+    evk.device_status(clear=True)
+    try:
+        evk.debug_set_spin_limit(1)
+        evk.model_decode_packed(cfg, P, cache, tok, 6, 40, logits)
+        torch.cuda.synchronize()
+        forced = evk.device_status(clear=True)
+    finally:
+        evk.debug_set_spin_limit(0)
+    assert forced & evk.STATUS_WAIT_TIMEOUT
+    tok[0] = first
+    evk.model_decode_packed(cfg, P, cache, tok, 6, 40, logits)
+    torch.cuda.synchronize()
+    assert evk.device_status(clear=True) == 0
+    stop = check_ids(list(from_dev(tok)), list(want_ids), want_logits)
+    if stop is None:
+        assert_close_f16(from_dev(logits), want_logits[-1], what="last logits after a timeout")
