@@ -173,34 +173,53 @@ DEV float group_max64(float x, int L) {
 // them back to back; agent-scope atomic loads got a wait after each).  Each
 // word is one naturally aligned 8-byte access, as the atomic load would be,
 // so its tag and payload come from the same store.
-DEV void poll(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail) {
+template <int NW>  // words per thread and round: n <= NW * NPOLL
+DEV void poll_n(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail) {
     const int tid = tid_now();
     const __amdgpu_buffer_rsrc_t r = buf_rsrc_u(box, (uint32_t)n * 8u);
     uint32_t pend = 0;
 #pragma unroll
-    for (int u = 0; u < PMAXW; ++u)
+    for (int u = 0; u < NW; ++u)
         if (tid + u * NPOLL < n) pend |= 1u << u;
-    int it = 0;
-    while (pend) {
-        u32x2 w[PMAXW];
+    // Two rounds in flight: round r + 1 is requested before round r is looked
+    // at, so a word is seen about half a load latency after it lands.  Every
+    // round requests NW words (those past n read as zeros), so that the wait
+    // for a round counts exactly the NW loads of the round after it.
+    auto issue = [&](u32x2* w) {
+        asm volatile("" ::: "memory");  // a new round: the words may have changed since the last one
 #pragma unroll
-        for (int u = 0; u < PMAXW; ++u)
-            if (u * NPOLL < n)  // uniform: words past n read as zeros
-                w[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                     r, (uint32_t)tid * 8u, (uint32_t)(u * NPOLL * 8), 16 | (1 << 31)));
+        for (int u = 0; u < NW; ++u)
+            w[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)tid * 8u,
+                                                                              (uint32_t)(u * NPOLL * 8), 16 | (1 << 31)));
+    };
+    auto take = [&](const u32x2* w) {
 #pragma unroll
-        for (int u = 0; u < PMAXW; ++u)
+        for (int u = 0; u < NW; ++u)
             if ((pend & (1u << u)) && w[u][1] == tag) {
                 dst[tid + u * NPOLL] = w[u][0];
                 pend &= ~(1u << u);
             }
-        if (!pend) break;
-        if (++it > limit) {
-            *s_fail = 1;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+    };
+    u32x2 wa[NW], wb[NW];
+    int it = 0;
+    issue(wa);
+    while (true) {
+        issue(wb);
+        take(wa);
+        if (!__any(pend != 0) || ++it > limit) break;
+        issue(wa);
+        take(wb);
+        if (!__any(pend != 0) || ++it > limit) break;
     }
+    if (pend) *s_fail = 1;
+}
+DEV void poll(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail) {
+    const int nw = (n + NPOLL - 1) / NPOLL;  // uniform
+    if (nw <= 1) poll_n<1>(box, n, tag, dst, limit, s_fail);
+    else if (nw <= 2) poll_n<2>(box, n, tag, dst, limit, s_fail);
+    else if (nw <= 4) poll_n<4>(box, n, tag, dst, limit, s_fail);
+    else if (nw <= 8) poll_n<8>(box, n, tag, dst, limit, s_fail);
+    else poll_n<PMAXW>(box, n, tag, dst, limit, s_fail);
 }
 
 // 16 bytes per lane from a buffer straight into LDS: lane i writes
@@ -311,13 +330,14 @@ DEV float rms_inv(const uint32_t* x, int K, float eps) {
     const int lane = tid_now() & 63;
     const int k8n = K / 8, full = k8n / 64, tail = full * 64 + lane;
     float ss = 0.0f;
+    // packed: clamp two fp16 values at once, then both squares into fp32
+    // (v_pk_min/max_f16, v_dot2_f32_f16)
     auto acc4 = [&](u32x4v v) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float a = fminf(fmaxf(lo_h(v[e]), -65504.0f), 65504.0f);
-            const float b = fminf(fmaxf(hi_h(v[e]), -65504.0f), 65504.0f);
-            ss = __builtin_fmaf(a, a, ss);
-            ss = __builtin_fmaf(b, b, ss);
+            const half2v c = __builtin_elementwise_min(__builtin_elementwise_max(as_h2(v[e]), half2v{-65504.0f16, -65504.0f16}),
+                                                       half2v{65504.0f16, 65504.0f16});
+            ss = __builtin_amdgcn_fdot2(c, c, ss, false);
         }
     };
     u32x4v vt = u32x4v{0u, 0u, 0u, 0u};
@@ -683,107 +703,133 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
                 }
             }
         } else if (cur.k == K_S2) {
-            // attention of head h over key split s; K, V rows of the split in W
+            // attention of head h over key split s; the split's cached K and V rows
+            // are in W ([key][dh] each, rows past the cached ones unused).  Wave w
+            // scores keys 16w..16w+15 (four lanes a key, dh/4 dimensions a lane)
+            // and forms its own softmax partial (m_w, l_w, o_w) with its lanes on
+            // the output dimensions; after one barrier the lanes of wave 0 merge
+            // the eight partials and the new key's term and store the block.
             const int h = wid / S, s = wid % S;
             const int per = (pos + 1 + S - 1) / S;
             const int k_lo = s * per, k_hi = min(pos + 1, k_lo + per), kc_hi = min(k_hi, pos);
             const bool has_new = k_hi == pos + 1;
-            const int kp = tid % PPK, kr = tid / PPK, KSL = PNT / PPK;
+            const int nk = max(0, kc_hi - k_lo);  // cached keys of the split
             const f16* Ks = W;
             const f16* Vs = W + KSPL * dh;
-            float qv[8];
+            const float c2 = att_scale * 1.4426950408889634f;  // scores in the base-2 domain
+            const int kb = (KSPL / PWV) * wave, kl = kb + (lane >> 2), part = lane & 3, dq = dh / 4;
+            float sc = 0.0f;
+            {
+                const f16* kr = Ks + kl * dh + part * dq;
+                const uint32_t* qw = mbuf + part * (dq / 2);
+                if (dq >= 8) {
+                    u32x4v kk[4], qq[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t w = mbuf[kp * 4 + e];
-                qv[2 * e] = lo_h(w);
-                qv[2 * e + 1] = hi_h(w);
-            }
-            // keys kr + KSL i of the split (KSL = 512 / (dh / 8) key slots);
-            // scores in the base-2 domain
-            constexpr int KPTM = 4;  // KSPL / KSL for dh = 128; 2, 1, 1 for dh = 64, 32, 16
-            const float c2 = att_scale * 1.4426950408889634f;
-            float sc[KPTM];
-            const int kpt = (KSPL + KSL - 1) / KSL;
-            float mx = -INFINITY;
+                    for (int j = 0; j < 4; ++j) {
+                        const int jj = j < dq / 8 ? j : 0;
+                        kk[j] = *reinterpret_cast<const u32x4v*>(kr + 8 * jj);
+                        qq[j] = *reinterpret_cast<const u32x4v*>(qw + 4 * jj);
+                    }
 #pragma unroll
-            for (int i = 0; i < KPTM; ++i) {
-                const int key = kr + KSL * i;
-                float acc = 0.0f;
-                if (i < kpt && key < KSPL) {
-                    const half8 kk = *reinterpret_cast<const half8*>(Ks + key * dh + kp * 8);
+                    for (int j = 0; j < 4; ++j) {
+                        float dj = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[e], (float)kk[e], acc);
+                        for (int e = 0; e < 4; ++e) dj = __builtin_amdgcn_fdot2(as_h2(qq[j][e]), as_h2(kk[j][e]), dj, false);
+                        sc += j < dq / 8 ? dj : 0.0f;
+                    }
+                } else {  // dh = 16: four dimensions a lane
+                    const uint2 kk = *reinterpret_cast<const uint2*>(kr);
+                    sc = __builtin_amdgcn_fdot2(as_h2(qw[0]), as_h2(kk.x), 0.0f, false);
+                    sc = __builtin_amdgcn_fdot2(as_h2(qw[1]), as_h2(kk.y), sc, false);
                 }
-                if (i < kpt) acc = group_sum(acc, PPK);
-                sc[i] = (i < kpt && key < KSPL && k_lo + key < kc_hi) ? acc * c2 : -INFINITY;
-                mx = fmaxf(mx, sc[i]);
             }
+            sc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sc), 0xB1, 0xF, 0xF, false));
+            sc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sc), 0x4E, 0xF, 0xF, false));
+            const bool live = kl < nk;
+            sc = live ? sc * c2 : -INFINITY;
+            const float mw = wave_maximum(sc);
+            const float pk = live ? __builtin_amdgcn_exp2f(sc - mw) : 0.0f;
+            const float lw = wave_total(part == 0 ? pk : 0.0f);
+            // p . v over the wave's keys: lane on dimension lane (dh <= 64) or on
+            // dimensions 2 lane, 2 lane + 1 (dh = 128); each key's p from its lanes
+            float o0 = 0.0f, o1 = 0.0f;
+            if (dh == 128) {
+                uint32_t vv[KSPL / PWV];
+#pragma unroll
+                for (int k = 0; k < KSPL / PWV; ++k) vv[k] = *reinterpret_cast<const uint32_t*>(Vs + (kb + k) * dh + 2 * lane);
+#pragma unroll
+                for (int k = 0; k < KSPL / PWV; ++k) {
+                    const float pkk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), 4 * k));
+                    const bool kv = kb + k < nk;
+                    o0 = __builtin_fmaf(pkk, kv ? lo_h(vv[k]) : 0.0f, o0);
+                    o1 = __builtin_fmaf(pkk, kv ? hi_h(vv[k]) : 0.0f, o1);
+                }
+            } else {
+                const int dl = lane < dh ? lane : 0;
+                f16 vv[KSPL / PWV];
+#pragma unroll
+                for (int k = 0; k < KSPL / PWV; ++k) vv[k] = Vs[(kb + k) * dh + dl];
+#pragma unroll
+                for (int k = 0; k < KSPL / PWV; ++k) {
+                    const float pkk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), 4 * k));
+                    o0 = __builtin_fmaf(pkk, kb + k < nk ? (float)vv[k] : 0.0f, o0);
+                }
+            }
+            float* ow = hs;  // [PWV][dh] partial outputs
+            const int d0 = dh == 128 ? 2 * lane : lane;
+            if (lane == 0) {
+                red[wave] = mw;
+                red[PWV + wave] = lw;
+            }
+            if (lane < dh) ow[wave * dh + d0] = o0;
+            if (dh == 128) ow[wave * dh + d0 + 1] = o1;
+            // the new key's score (q . k of pos), in every wave
             float s_new = -INFINITY;
             if (has_new) {
                 float acc = 0.0f;
-                for (int c = lane; c < dh; c += 64) {
-                    const uint32_t qw = mbuf[c / 2], kw = mbuf[dh / 2 + c / 2];
-                    acc += ((c & 1) ? hi_h(qw) : lo_h(qw)) * ((c & 1) ? hi_h(kw) : lo_h(kw));
-                }
+                if (lane < dh) acc = (d0 & 1 ? hi_h(mbuf[d0 / 2]) : lo_h(mbuf[d0 / 2])) *
+                                     (d0 & 1 ? hi_h(mbuf[dh / 2 + d0 / 2]) : lo_h(mbuf[dh / 2 + d0 / 2]));
+                if (dh == 128) acc += hi_h(mbuf[d0 / 2]) * hi_h(mbuf[dh / 2 + d0 / 2]);
                 s_new = wave_total(acc) * c2;
             }
-            mx = fmaxf(wave_maximum(mx), s_new);
-            if (lane == 0) red[wave] = mx;
             __syncthreads();
-            mx = red[0];
+            if (tid < min(dh, 64)) {
+                float M = s_new;
 #pragma unroll
-            for (int w = 1; w < PWV; ++w) mx = fmaxf(mx, red[w]);
-            // this thread's keys' p, their sum (once per key) and p . v over its dims
-            float ps = 0.0f, o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                for (int w = 0; w < PWV; ++w)
+                    if (red[PWV + w] > 0.0f) M = fmaxf(M, red[w]);
+                float l = 0.0f, a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-            for (int i = 0; i < KPTM; ++i) {
-                const int key = kr + KSL * i;
-                const float pe = sc[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[i] - mx);
-                if (kp == 0) ps += pe;
-                if (pe != 0.0f) {
-                    const half8 vv = *reinterpret_cast<const half8*>(Vs + key * dh + kp * 8);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o8[e] = __builtin_fmaf(pe, (float)vv[e], o8[e]);
+                for (int w = 0; w < PWV; ++w) {
+                    const float lw2 = red[PWV + w];
+                    const float f = lw2 > 0.0f ? __builtin_amdgcn_exp2f(red[w] - M) : 0.0f;
+                    l = __builtin_fmaf(lw2, f, l);
+                    a0 = __builtin_fmaf(f, ow[w * dh + d0], a0);
+                    if (dh == 128) a1 = __builtin_fmaf(f, ow[w * dh + d0 + 1], a1);
                 }
-            }
-            ps = wave_total(ps);
-            // the key slots' partial outputs through LDS: [slot][dh]
-            *reinterpret_cast<floatx4*>(hs + kr * dh + kp * 8) = floatx4{o8[0], o8[1], o8[2], o8[3]};
-            *reinterpret_cast<floatx4*>(hs + kr * dh + kp * 8 + 4) = floatx4{o8[4], o8[5], o8[6], o8[7]};
-            if (lane == 0) red[PWV + wave] = ps;
-            __syncthreads();
-            // output dim c summed over the key slots by GS adjacent lanes, each
-            // taking every GS-th slot (GS = 512 / dh, at most 16), then DPP
-            const int GS = min(PNT / dh, 16), c = tid / GS, g = tid % GS;
-            const int nsl = min(KSL, KSPL);
-            float o = 0.0f;
-            if (c < dh) {
-#pragma unroll 8
-                for (int k2 = g; k2 < nsl; k2 += GS) o += hs[k2 * dh + c];
-            }
-            o = group_sum(o, GS);
-            if (c < dh && g == 0) {
-                float l_sum = 0.0f;
-#pragma unroll
-                for (int w = 0; w < PWV; ++w) l_sum += red[PWV + w];
                 if (has_new) {
-                    const float pn = __builtin_amdgcn_exp2f(s_new - mx);
-                    const uint32_t vw = mbuf[dh + c / 2];
-                    o += pn * ((c & 1) ? hi_h(vw) : lo_h(vw));
-                    l_sum += pn;
+                    const float pn = __builtin_amdgcn_exp2f(s_new - M);
+                    const uint32_t vw = mbuf[dh + d0 / 2];
+                    a0 = __builtin_fmaf(pn, d0 & 1 ? hi_h(vw) : lo_h(vw), a0);
+                    if (dh == 128) a1 = __builtin_fmaf(pn, hi_h(vw), a1);
+                    l += pn;
                 }
-                yo[c] = l_sum > 0.0f ? o / l_sum : 0.0f;
-                if (c == 0) {
-                    yo[dh] = mx * 0.6931471805599453f;  // natural-log maximum, as the merge expects
-                    yo[dh + 1] = l_sum;
+                const float r0 = l > 0.0f ? a0 / l : 0.0f, r1 = l > 0.0f ? a1 / l : 0.0f;
+                uint64_t* blk = a.mb + a.o_att + p * a.par + (s * H + h) * ablk;
+                const uint32_t tg = tag_of(t, k0 + 1);
+                if (dh == 128) {
+                    mb_st(blk + 2 + tid, tg, pack2(r0, r1));
+                } else {
+                    // dimension pairs: the odd lane's value to its even neighbour
+                    const float nb = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, r0), 0xB1, 0xF, 0xF, false));
+                    if (!(tid & 1)) mb_st(blk + 2 + tid / 2, tg, pack2(r0, nb));
+                }
+                if (tid == 0) {
+                    mb_st(blk, tg, __builtin_bit_cast(uint32_t, M * 0.6931471805599453f));  // natural-log maximum
+                    mb_st(blk + 1, tg, __builtin_bit_cast(uint32_t, l));
                 }
             }
-            __syncthreads();
-            uint64_t* blk = a.mb + a.o_att + p * a.par + (s * H + h) * ablk;
-            const uint32_t tg = tag_of(t, k0 + 1);
-            if (tid < dh / 2) mb_st(blk + 2 + tid, tg, pack2(yo[2 * tid], yo[2 * tid + 1]));
-            else if (tid == dh / 2) mb_st(blk, tg, __builtin_bit_cast(uint32_t, yo[dh]));
-            else if (tid == dh / 2 + 1) mb_st(blk + 1, tg, __builtin_bit_cast(uint32_t, yo[dh + 1]));
         } else if (cur.k == K_S3) {
             // merge the splits; x1 = x + attn . Wo.  Split s of head h weighs
             // l_s e^(m_s - M_h) / sum over the head's splits (one exponential per
