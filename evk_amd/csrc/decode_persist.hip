@@ -57,6 +57,7 @@ constexpr int PMAXW = 16;          // mailbox words one polling thread takes (<=
 constexpr int NBUF = 3;            // LDS weight slots: a stage's slice is requested two stages ahead
 constexpr int KSPL = 128;          // keys per attention split
 constexpr uint32_t kWrapAt = 0xFFF00000u;
+constexpr int RSQ = 32;            // red[RSQ, RSQ + 4): the polling waves' sums of squares
 constexpr int YO = 144;            // stage output floats (>= head rows per slot, >= dh + 2)
 
 __device__ unsigned g_dec_status;
@@ -108,6 +109,9 @@ DEV uint32_t pack2(float a, float b) { return (uint32_t)f2h(a) | ((uint32_t)f2h(
 DEV float lo_h(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
 DEV float hi_h(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+DEV half2v as_h2(uint32_t w) { return __builtin_bit_cast(half2v, w); }
 // Sum over groups of L = 16, 32 or 64 lanes, complete in each group's last
 // lane: DPP within rows of 16, then row_bcast:15 and row_bcast:31 (no LDS
 // round trip, unlike a cross-row shuffle).
@@ -173,8 +177,12 @@ DEV float group_max64(float x, int L) {
 // them back to back; agent-scope atomic loads got a wait after each).  Each
 // word is one naturally aligned 8-byte access, as the atomic load would be,
 // so its tag and payload come from the same store.
-template <int NW>  // words per thread and round: n <= NW * NPOLL
-DEV void poll_n(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail) {
+// With SSQ, the waiting waves also form rms_norm's sum of squares of the
+// words' fp16 values (clamped, rms_norm.comp): each thread over its own words
+// in word order, then each wave's total into ssq[wave], so that the sum is
+// the same on every run.
+template <int NW, bool SSQ>  // words per thread and round: n <= NW * NPOLL
+DEV void poll_n(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail, float* ssq) {
     const int tid = tid_now();
     const __amdgpu_buffer_rsrc_t r = buf_rsrc_u(box, (uint32_t)n * 8u);
     uint32_t pend = 0;
@@ -192,11 +200,15 @@ DEV void poll_n(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int lim
             w[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (uint32_t)tid * 8u,
                                                                               (uint32_t)(u * NPOLL * 8), 16 | (1 << 31)));
     };
+    uint32_t val[NW];
+#pragma unroll
+    for (int u = 0; u < NW; ++u) val[u] = 0u;
     auto take = [&](const u32x2* w) {
 #pragma unroll
         for (int u = 0; u < NW; ++u)
             if ((pend & (1u << u)) && w[u][1] == tag) {
                 dst[tid + u * NPOLL] = w[u][0];
+                if (SSQ) val[u] = w[u][0];
                 pend &= ~(1u << u);
             }
     };
@@ -212,14 +224,35 @@ DEV void poll_n(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int lim
         if (!__any(pend != 0) || ++it > limit) break;
     }
     if (pend) *s_fail = 1;
+    if (SSQ) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NW; ++u) {  // words past n hold zero
+            const half2v c = __builtin_elementwise_min(
+                __builtin_elementwise_max(as_h2(val[u]), half2v{-65504.0f16, -65504.0f16}), half2v{65504.0f16, 65504.0f16});
+            ss = __builtin_amdgcn_fdot2(c, c, ss, false);
+        }
+        ss = wave_total(ss);
+        if ((tid & 63) == 0) ssq[tid >> 6] = ss;
+    }
 }
-DEV void poll(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail) {
+// ssq: see poll_n; given only for n <= 4 NPOLL
+DEV void poll(const uint64_t* box, int n, uint32_t tag, uint32_t* dst, int limit, int* s_fail, float* ssq) {
     const int nw = (n + NPOLL - 1) / NPOLL;  // uniform
-    if (nw <= 1) poll_n<1>(box, n, tag, dst, limit, s_fail);
-    else if (nw <= 2) poll_n<2>(box, n, tag, dst, limit, s_fail);
-    else if (nw <= 4) poll_n<4>(box, n, tag, dst, limit, s_fail);
-    else if (nw <= 8) poll_n<8>(box, n, tag, dst, limit, s_fail);
-    else poll_n<PMAXW>(box, n, tag, dst, limit, s_fail);
+    if (ssq) {
+        if (nw <= 2) poll_n<2, true>(box, n, tag, dst, limit, s_fail, ssq);
+        else poll_n<4, true>(box, n, tag, dst, limit, s_fail, ssq);
+    } else if (nw <= 1) {
+        poll_n<1, false>(box, n, tag, dst, limit, s_fail, ssq);
+    } else if (nw <= 2) {
+        poll_n<2, false>(box, n, tag, dst, limit, s_fail, ssq);
+    } else if (nw <= 4) {
+        poll_n<4, false>(box, n, tag, dst, limit, s_fail, ssq);
+    } else if (nw <= 8) {
+        poll_n<8, false>(box, n, tag, dst, limit, s_fail, ssq);
+    } else {
+        poll_n<PMAXW, false>(box, n, tag, dst, limit, s_fail, ssq);
+    }
 }
 
 // 16 bytes per lane from a buffer straight into LDS: lane i writes
@@ -250,9 +283,6 @@ DEV void wait_vm_le(int n) {
     __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-DEV half2v as_h2(uint32_t w) { return __builtin_bit_cast(half2v, w); }
 // h = fp16(clamp(x) * inv) on a word of two fp16 values (rms_norm.comp's output)
 DEV uint32_t norm_w(uint32_t w, float inv) {
     const float a = fminf(fmaxf(lo_h(w), -65504.0f), 65504.0f) * inv;
@@ -359,6 +389,12 @@ DEV float rms_inv(const uint32_t* x, int K, float eps) {
 // the caller's barrier publishes it.
 DEV void rms_norm_words(const uint32_t* x, uint32_t* hn, int K, float eps) {
     const float inv = rms_inv(x, K, eps);
+    for (int i = tid_now(); i < K / 2; i += PNT) hn[i] = norm_w(x[i], inv);
+}
+// the same from the four polling waves' sums of squares (poll_n with SSQ)
+DEV void rms_norm_words_ssq(const uint32_t* x, uint32_t* hn, int K, float eps, const float* ssq) {
+    const float ss = ((ssq[0] + ssq[1]) + ssq[2]) + ssq[3];
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
     for (int i = tid_now(); i < K / 2; i += PNT) hn[i] = norm_w(x[i], inv);
 }
 
@@ -574,6 +610,9 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
     };
 
     const bool streamer = (int)threadIdx.x >= NPOLL;
+    // rms_norm's sums of squares formed by the polls of x (up to 4 words a poller)
+    const bool ssq_poll = d / 2 <= 4 * NPOLL;
+    static_assert(NPOLL == 4 * 64, "four polling waves");
     Cur cur{0, 0, K_S1, 0};
     Cur c1 = next(cur), c2 = next(c1);
     // this wave's loads of the stage, the next one and the one after
@@ -601,10 +640,12 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             int nw = 0;
             uint32_t tg = 0;
             uint32_t* dst = mbuf;
+            float* sq = nullptr;  // rms_norm's sum of squares of x, formed while polling
             switch (cur.k) {
                 case K_S1:
                     if (l > 0) {
                         box = a.mb + a.o_x2 + (p ^ 1) * a.par, nw = d / 2, tg = tag_of(t, k0 - 1), dst = xw;
+                        sq = ssq_poll ? red + RSQ : nullptr;
                     } else if (t > 0) {
                         box = a.mb + a.o_cand, nw = 2 * G, tg = tag_of(t - 1, HEAD);
                     }
@@ -619,14 +660,18 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
                     break;
                 }
                 case K_S3: box = a.mb + a.o_att + p * a.par, nw = S * H * ablk, tg = tag_of(t, k0 + 1); break;
-                case K_S4: box = a.mb + a.o_x1 + p * a.par, nw = d / 2, tg = tag_of(t, k0 + 2), dst = xw; break;
+                case K_S4:
+                    box = a.mb + a.o_x1 + p * a.par, nw = d / 2, tg = tag_of(t, k0 + 2), dst = xw;
+                    sq = ssq_poll ? red + RSQ : nullptr;
+                    break;
                 case K_S5: box = a.mb + a.o_gh + p * a.par, nw = hid / 2, tg = tag_of(t, k0 + 3), dst = hw; break;
                 default:
                     if (cur.sub == 0) {
                         box = a.mb + a.o_x2 + ((a.L - 1) & 1) * a.par, nw = d / 2, tg = tag_of(t, HEAD - 1), dst = xw;
+                        sq = ssq_poll ? red + RSQ : nullptr;
                     }
             }
-            if (nw > 0) poll(box, nw, tg, dst, a.spin_limit, &s_fail);
+            if (nw > 0) poll(box, nw, tg, dst, a.spin_limit, &s_fail, sq);
         } else {
             // this stage's slice is in LDS once only the two later ones are in flight
             wait_vm_le(n1 + n2);
@@ -669,7 +714,8 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
                     for (int i = tid; i < d / 2; i += NPOLL) xw[i] = reinterpret_cast<const uint32_t*>(er)[i];
                 __syncthreads();
             }  // (otherwise the poll wrote x to xw)
-            rms_norm_words(xw, hw, d, a.eps);
+            if (l > 0 && ssq_poll) rms_norm_words_ssq(xw, hw, d, a.eps, red + RSQ);
+            else rms_norm_words(xw, hw, d, a.eps);
             __syncthreads();
             dot_lds<32>(W, d, 2 * (p1_hi - p1_lo), hw, yo);
             __syncthreads();
@@ -886,7 +932,8 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             }
         } else if (cur.k == K_S4) {
             // x1 (in xw from the poll), rms_norm, gelu(h . W1)
-            rms_norm_words(xw, hw, d, a.eps);
+            if (ssq_poll) rms_norm_words_ssq(xw, hw, d, a.eps, red + RSQ);
+            else rms_norm_words(xw, hw, d, a.eps);
             __syncthreads();
             dot_lds<32>(W, d, 2 * (p4_hi - p4_lo), hw, yo);
             __syncthreads();
@@ -908,7 +955,8 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             // LM head slot: logits of rows [r0, r0 + nr); the step's candidate
             // after the last slot
             if (cur.sub == 0) {  // x2 in xw from the poll; hw keeps rms_norm(x2) over the slots
-                rms_norm_words(xw, hw, d, a.eps);
+                if (ssq_poll) rms_norm_words_ssq(xw, hw, d, a.eps, red + RSQ);
+                else rms_norm_words(xw, hw, d, a.eps);
                 __syncthreads();
                 hbv = -3.402823466e+38f;
                 hbr = 0u;
@@ -947,7 +995,7 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
 
     // ---- the last step's token ----
     if (wid == 0) {
-        if (!streamer) poll(a.mb + a.o_cand, 2 * G, tag_of(a.n - 1, HEAD), mbuf, a.spin_limit, &s_fail);
+        if (!streamer) poll(a.mb + a.o_cand, 2 * G, tag_of(a.n - 1, HEAD), mbuf, a.spin_limit, &s_fail, nullptr);
         __syncthreads();
         if (s_fail) {
             fail();
@@ -1013,8 +1061,10 @@ int plan_for(const evkhip_model_cfg& c, int cus, int lds_max, Plan* out) {
     // every workgroup writes at least one word in S1, S4 and the head
     p.G = std::min(std::min(cus, 3 * d / 2), std::min(hid / 2, (int)c.vocab));
     p.S_max = ((int)c.max_seq + KSPL - 1) / KSPL;
-    // Wo and W2 columns: 8 (Wo) and 6 (W2) per workgroup, in pairs
-    p.R3 = 8;
+    // Wo and W2 columns: 16 (Wo) and 6 (W2) per workgroup, in pairs.  Fewer
+    // S3 workgroups poll the large attention mailbox (measured: 16 beats 8,
+    // 12 and 24 at C4); a W2 slice of 6 rows x hidden already fills a slot.
+    p.R3 = 16;
     p.G3 = (d + p.R3 - 1) / p.R3;
     p.R5 = 6;
     p.G5 = (d + p.R5 - 1) / p.R5;
