@@ -1329,8 +1329,21 @@ template <int DH, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_bwd_kvq(FlashArgs p, float* part_ws, int parts_per_batch, int n_kv) {
     constexpr int KVB = KvLayout<DH>::LDS_BYTES, QB = DqLayout<DH>::LDS_BYTES;
     __shared__ __attribute__((aligned(16))) char lds[KVB > QB ? KVB : QB];
-    if ((int)blockIdx.x < n_kv) bwd_kv_body<DH, CAUSAL>(p, part_ws, parts_per_batch, blockIdx.x, lds);
-    else bwd_q_body<DH, CAUSAL>(p, blockIdx.x - n_kv, lds);
+    if ((int)blockIdx.x < n_kv) {
+        // Workgroup i runs on XCD i % 8.  When the batches divide the XCDs
+        // evenly, XCD x takes the dK/dV parts of batch x / (8 / B) only
+        // (every (8 / B)-th part, heavy key blocks first), so the key blocks
+        // that re-read a batch's Q, dO and O rows find them in that XCD's L2.
+        int blk = blockIdx.x;
+        const int xpb = p.B > 0 && 8 % p.B == 0 ? 8 / p.B : 0;
+        if (xpb > 0 && parts_per_batch % xpb == 0 && n_kv == p.B * parts_per_batch) {
+            const int x = blk % 8, i = blk / 8;
+            blk = (x / xpb) * parts_per_batch + i * xpb + x % xpb;
+        }
+        bwd_kv_body<DH, CAUSAL>(p, part_ws, parts_per_batch, blk, lds);
+    } else {
+        bwd_q_body<DH, CAUSAL>(p, blockIdx.x - n_kv, lds);
+    }
 }
 
 // lse2_rows / d_rows from a saved LSE and O: D_i = rowsum(dO_i * O_i).
