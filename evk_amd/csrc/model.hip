@@ -25,12 +25,58 @@ __global__ __launch_bounds__(256) void copy_k(const u32x4* src, u32x4* dst, int6
     if (i < n16) dst[i] = src[i];
 }
 
+// Batched prefill: rows i of qkv (n, 3d) are positions pos0 + i.  q and k
+// are rotated with rope_k's formula (pairs within a head, fp32, one fp16
+// rounding), q, k, v are regrouped per head as (heads, n, dh) for the flash
+// kernels, and the k, v rows go to the cache at their positions.  One thread
+// per pair of columns.
+__global__ __launch_bounds__(256) void prefill_split_k(const f16* qkv, int n, int d, int dh, float base, int pos0,
+                                                       f16* Qh, f16* Kh, f16* Vh, f16* Kc, f16* Vc) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int pairs = d / 2;
+    if (gid >= (int64_t)n * pairs) return;
+    const int c = 2 * (int)(gid % pairs), i = (int)(gid / pairs);
+    const int h = c / dh, j = c % dh, pp = j / 2;
+    const f16* row = qkv + (int64_t)i * 3 * d;
+    const float inv_freq = powf(base, -2.0f * (float)pp / (float)dh);
+    float sn, cs;
+    sincosf((float)(pos0 + i) * inv_freq, &sn, &cs);
+    const int64_t o = ((int64_t)h * n + i) * dh + j, oc = (int64_t)(pos0 + i) * d + c;
+    float x0 = (float)row[c], x1 = (float)row[c + 1];
+    Qh[o] = (f16)(x0 * cs - x1 * sn);
+    Qh[o + 1] = (f16)(x0 * sn + x1 * cs);
+    x0 = (float)row[d + c];
+    x1 = (float)row[d + c + 1];
+    const f16 k0 = (f16)(x0 * cs - x1 * sn), k1 = (f16)(x0 * sn + x1 * cs);
+    Kh[o] = k0;
+    Kh[o + 1] = k1;
+    Kc[oc] = k0;
+    Kc[oc + 1] = k1;
+    const f16 v0 = row[2 * d + c], v1 = row[2 * d + c + 1];
+    Vh[o] = v0;
+    Vh[o + 1] = v1;
+    Vc[oc] = v0;
+    Vc[oc + 1] = v1;
+}
+
+// (heads, n, dh) -> (n, heads * dh), 16 bytes per thread
+__global__ __launch_bounds__(256) void prefill_merge_k(const f16* Oh, f16* A, int n, int d, int dh) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int c8 = d / 8;
+    if (gid >= (int64_t)n * c8) return;
+    const int c = 8 * (int)(gid % c8), i = (int)(gid / c8);
+    const int h = c / dh, j = c % dh;
+    *reinterpret_cast<u32x4*>(A + (int64_t)i * d + c) =
+        *reinterpret_cast<const u32x4*>(Oh + ((int64_t)h * n + i) * dh + j);
+}
+
 struct ModelWs {
     f16* buf = nullptr;
     size_t elems = 0;
 };
 ModelWs g_ws;   // unfused path (fp16 elements)
 ModelWs g_fws;  // fused path (bytes in `elems`)
+ModelWs g_pws;  // batched prefill (fp16 elements)
 // Counters of the fused kernels: their own grow-only array, zeroed when it
 // grows; every launch leaves them at zero, so any configuration can reuse them.
 unsigned* g_fcnt = nullptr;
@@ -648,6 +694,8 @@ void model_free_workspace() {
     g_ws = ModelWs{};
     if (g_fws.buf) (void)hipFree(g_fws.buf);
     g_fws = ModelWs{};
+    if (g_pws.buf) (void)hipFree(g_pws.buf);
+    g_pws = ModelWs{};
     if (g_fcnt) (void)hipFree(g_fcnt);
     g_fcnt = nullptr;
     g_fcnt_n = 0;
@@ -811,6 +859,92 @@ int run_tokens_fused(const evkhip_model_cfg& c, const f16* E, const f16* Wout, u
 // Validates cfg/buffers and runs n tokens.  feed != null: token s is feed[s],
 // only the last step runs the LM head (into ids[0]); otherwise token s is
 // ids[s] and every step writes ids[s+1].
+// Prefill of a prompt at positions 0..n-1 as whole-sequence ops (the
+// reference evaluates the sequence this way, evk_ai.h:670-712): per layer
+// rms_norm over the n rows, X.Wqkv on the MFMA GEMM, rope and the cache rows,
+// causal flash attention per head (heads as the batch), X.Wo, residual,
+// rms_norm, gelu(X.W1).W2, residual; then the last row's logits and greedy id.
+// Same op sequence and fp16 rounding points as the token loop; the GEMMs sum
+// in another order.  Returns 1 when the shape is not taken (the token loop
+// serves it), an evkhip error code otherwise.
+int run_prefill_batched(const evkhip_model_cfg& c, const f16* E, const f16* Wout, uint64_t per_layer, f16* cache_h,
+                        const uint16_t* feed, uint16_t* ids, uint32_t n, f16* logits, hipStream_t st) {
+    const int d = (int)c.d, hid = (int)c.hidden, H = (int)c.heads, dh = (int)c.dh;
+    if (n < 16 || !flash_mfma_head(c.dh) || dh % 8 || (int64_t)n * 3 * d * 2 >= INT32_MAX ||
+        (int64_t)n * hid * 2 >= INT32_MAX)
+        return 1;
+    const size_t nd = (size_t)n * d, nh = (size_t)n * hid;
+    // X, Hn, QKV (3), Qh, Kh, Vh, Oh, A, T: 11 n d; HH, HG: 2 n hidden
+    const size_t need = 11 * nd + 2 * nh;
+    if (need * sizeof(f16) > ((size_t)1 << 31)) return 1;
+    if (need > g_pws.elems) {
+        if (g_pws.buf) EVK_HIP(hipFree(g_pws.buf));
+        g_pws.buf = nullptr;
+        g_pws.elems = 0;
+        EVK_HIP(hipMalloc(&g_pws.buf, need * sizeof(f16)));
+        g_pws.elems = need;
+    }
+    f16* X = g_pws.buf;
+    f16* Hn = X + nd;
+    f16* QKV = Hn + nd;  // 3 nd
+    f16* Qh = QKV + 3 * nd;
+    f16* Kh = Qh + nd;
+    f16* Vh = Kh + nd;
+    f16* Oh = Vh + nd;
+    f16* A = Oh + nd;
+    f16* T = A + nd;
+    f16* HH = T + nd;
+    f16* HG = HH + nh;
+    auto gemm = [&](const f16* a, const f16* b, f16* out, int M, int N, int K) {
+        GemmArgs g{};
+        g.A = a;
+        g.B = b;
+        g.C = out;
+        g.M = M;
+        g.N = N;
+        g.K = K;
+        return gemm_dispatch(g, 1, false, false, true, st);
+    };
+    const unsigned g_split = (unsigned)(((int64_t)n * (d / 2) + 255) / 256);
+    const unsigned g_merge = (unsigned)(((int64_t)n * (d / 8) + 255) / 256);
+    CHECK(embed_launch(E, feed, X, n, d, (int)c.vocab, st));
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const f16* Wqkv = E + (uint64_t)c.vocab * d + l * per_layer;
+        const f16* Wo = Wqkv + (uint64_t)d * 3 * d;
+        const f16* W1 = Wo + (uint64_t)d * d;
+        const f16* W2 = W1 + (uint64_t)d * hid;
+        f16* Kc = cache_h + (uint64_t)l * 2 * c.max_seq * d;
+        f16* Vc = Kc + (uint64_t)c.max_seq * d;
+        CHECK(rms_norm_launch(X, Hn, n, d, c.eps, st));
+        CHECK(gemm(Hn, Wqkv, QKV, (int)n, 3 * d, d));
+        hipLaunchKernelGGL(prefill_split_k, dim3(g_split), dim3(256), 0, st, QKV, (int)n, d, dh, c.rope_base, 0, Qh,
+                           Kh, Vh, Kc, Vc);
+        FlashArgs fa{};
+        fa.q = Qh;
+        fa.k = Kh;
+        fa.v = Vh;
+        fa.out = Oh;
+        fa.B = H;
+        fa.H = 1;
+        fa.N = (int)n;
+        CHECK(flash_forward(fa, dh, true, true, st));
+        hipLaunchKernelGGL(prefill_merge_k, dim3(g_merge), dim3(256), 0, st, Oh, A, (int)n, d, dh);
+        CHECK(gemm(A, Wo, T, (int)n, d, d));
+        CHECK(add_launch(X, T, X, (int64_t)nd, st));
+        CHECK(rms_norm_launch(X, Hn, n, d, c.eps, st));
+        CHECK(gemm(Hn, W1, HH, (int)n, hid, d));
+        CHECK(gelu_launch(HH, HG, (int64_t)nh, st));
+        CHECK(gemm(HG, W2, T, (int)n, d, hid));
+        CHECK(add_launch(X, T, X, (int64_t)nd, st));
+    }
+    // the last position's logits and greedy id (rms_norm of its row into Hn's first row)
+    CHECK(rms_norm_launch(X + (size_t)(n - 1) * d, Hn, 1, d, c.eps, st));
+    CHECK(gemm(Hn, Wout, logits, 1, (int)c.vocab, d));
+    CHECK(greedy_launch(logits, ids, 1, 1, (int)c.vocab, 0, 0, (int)c.vocab, st));
+    EVK_HIP(hipGetLastError());
+    return EVKHIP_OK;
+}
+
 int run_tokens(const evkhip_model_cfg* cfg, const void* weights, void* cache, const uint16_t* feed,
                uint16_t* ids, uint32_t n, uint32_t pos0, void* logits, hipStream_t st) {
     EVK_RETURN_IF(!cfg || !weights || !cache || !ids || !logits, EVKHIP_ERR_INVALID_ARG,
@@ -850,6 +984,10 @@ int run_tokens(const evkhip_model_cfg* cfg, const void* weights, void* cache, co
     W.per_layer = (uint64_t)d * 3 * d + (uint64_t)d * d + (uint64_t)d * hid + (uint64_t)hid * d;
     W.Wout = W.E + (uint64_t)c.vocab * d + c.layers * W.per_layer;
     f16* cache_h = (f16*)cache;
+    if (feed && pos0 == 0) {  // a prompt from position 0: whole-sequence ops
+        const int r = run_prefill_batched(c, W.E, W.Wout, W.per_layer, cache_h, feed, ids, n, (f16*)logits, st);
+        if (r != 1) return r;
+    }
     // the fused attention gives each key dh/16 lanes of one wave (a power of two)
     // (the fused GEMVs keep their input vector in LDS: K floats next to 33 KB
     // of reduction space, within 64 KB per workgroup)
