@@ -840,19 +840,34 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             }
             __syncthreads();
             if (tid < min(dh, 64)) {
-                float M = s_new;
-#pragma unroll
-                for (int w = 0; w < PWV; ++w)
-                    if (red[PWV + w] > 0.0f) M = fmaxf(M, red[w]);
-                float l = 0.0f, a0 = 0.0f, a1 = 0.0f;
+                // every partial requested at once, then trees (no serial chains)
+                float mw8[PWV], lw8[PWV], oa[PWV], ob[PWV];
 #pragma unroll
                 for (int w = 0; w < PWV; ++w) {
-                    const float lw2 = red[PWV + w];
-                    const float f = lw2 > 0.0f ? __builtin_amdgcn_exp2f(red[w] - M) : 0.0f;
-                    l = __builtin_fmaf(lw2, f, l);
-                    a0 = __builtin_fmaf(f, ow[w * dh + d0], a0);
-                    if (dh == 128) a1 = __builtin_fmaf(f, ow[w * dh + d0 + 1], a1);
+                    mw8[w] = red[w];
+                    lw8[w] = red[PWV + w];
+                    oa[w] = ow[w * dh + d0];
+                    ob[w] = dh == 128 ? ow[w * dh + d0 + 1] : 0.0f;
                 }
+                float mm[PWV];
+#pragma unroll
+                for (int w = 0; w < PWV; ++w) mm[w] = lw8[w] > 0.0f ? mw8[w] : -INFINITY;
+                const float M = fmaxf(fmaxf(fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3])),
+                                            fmaxf(fmaxf(mm[4], mm[5]), fmaxf(mm[6], mm[7]))),
+                                      s_new);
+                float lf[PWV], af[PWV], bf[PWV];
+#pragma unroll
+                for (int w = 0; w < PWV; ++w) {
+                    const float f = lw8[w] > 0.0f ? __builtin_amdgcn_exp2f(mw8[w] - M) : 0.0f;
+                    lf[w] = lw8[w] * f;
+                    af[w] = f * oa[w];
+                    bf[w] = f * ob[w];
+                }
+                auto tree = [](const float* v) {
+                    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                };
+                static_assert(PWV == 8, "eight waves");
+                float l = tree(lf), a0 = tree(af), a1 = tree(bf);
                 if (has_new) {
                     const float pn = __builtin_amdgcn_exp2f(s_new - M);
                     const uint32_t vw = mbuf[dh + d0 / 2];
