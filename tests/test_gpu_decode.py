@@ -363,3 +363,30 @@ def test_decode_packed_wait_timeout_is_reported(dev, orc):
     stop = check_ids(list(from_dev(tok)), list(want_ids), want_logits)
     if stop is None:
         assert_close_f16(from_dev(logits), want_logits[-1], what="last logits after a timeout")
+
+
+def test_prefill_in_two_parts(dev, orc):
+    """A prompt prefilled in two calls: the first part from position 0 runs as
+    whole-sequence ops (batched GEMMs, causal flash per head), the second part
+    at pos0 > 0 through the token loop.  The cache, the logits after the last
+    prompt token and the next id match the oracle's single prefill (ids
+    except at near-ties)."""
+    import torch
+    import evk_amd as evk
+    kw = dict(vocab=512, d=128, heads=2, layers=2, hidden=256, max_seq=96)
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=361, std=0.1)
+    prompt = orc.tokens_u16(70, 362, kw["vocab"])
+    W = to_dev(w, dev)
+    cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
+    tok = torch.zeros(2, dtype=torch.int16, device=dev)
+    logits = torch.empty(cfg.vocab, dtype=torch.float16, device=dev)
+    feed = torch.from_numpy(prompt.view(np.int16)).to(dev)
+    evk.model_prefill(cfg, W, cache, feed[:48], 0, tok, logits)
+    evk.model_prefill(cfg, W, cache, feed[48:], 48, tok, logits)
+    torch.cuda.synchronize()
+    want_ids, want_cache, want_logits = orc.model_generate(ocfg, w, prompt, 0, return_logits=True)
+    assert_close_f16(from_dev(logits), want_logits[0], what="logits after the prompt")
+    stop = check_ids([int(from_dev(tok)[0])], [int(want_ids[0])], want_logits)
+    if stop is None:
+        assert_close_f16(from_dev(cache), want_cache, what="kv cache")
