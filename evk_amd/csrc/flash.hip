@@ -943,8 +943,13 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
                 if (which) dsum = dot8(as_half8(pr[i]), as_half8(po));
             }
         }
-#pragma unroll
-        for (int o = 1; o < DH / 8; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
+        // the DH/8 lanes of a row are adjacent (a quad or two): DPP sums
+        dsum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dsum), 0xB1, 0xF, 0xF, false));
+        if (DH / 8 >= 4)
+            dsum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dsum), 0x4E, 0xF, 0xF, false));
+        if (DH / 8 >= 8)
+            dsum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dsum), 0x141, 0xF, 0xF, false));
+        static_assert(DH / 8 <= 8, "a row's lanes within a half row");
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int pc = threadIdx.x + 256 * i;
