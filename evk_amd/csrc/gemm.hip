@@ -210,7 +210,10 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled(GemmArgs p) {
 // ---- MFMA kernel: BM x BN tiles; 4 waves of (BM/2) x (BN/2), or for 256x256
 // tiles 8 waves of 128 x 64 (two waves per SIMD: one wave's LDS reads and
 // waits overlap the other's MFMAs; measured 2-5 % faster than 4 waves of
-// 128 x 128 at 4096^3 and QKV, while 4 waves of 64 x 128 were slower) -------
+// 128 x 128 at 4096^3 and QKV, while 4 waves of 64 x 128 were slower).
+// 64x64 tiles of a grid that fits the CUs once with a long K run go as four
+// K groups of 4 waves (16 waves), whose fp32 sums are added in group order
+// in LDS, so the result does not depend on timing: 1024^3 8.6 -> 7.1 us ----
 // v_mfma_f32_16x16x32_f16 (lane l: A row l%16 / B column l%16, k 8(l/16)..+8;
 // D column l%16, rows 4(l/16)..+3).  Each operand tile of BK = 64 along K
 // goes from global memory straight into LDS (buffer_load_dwordx4 ... lds: a
@@ -309,16 +312,18 @@ DEV void wait_vmcnt(int n) {
     }
 }
 
-template <int BM, int BN, bool TA, bool TB, int NWV = 4>
-__global__ __launch_bounds__(64 * NWV, 1) void gemm_mfma(GemmArgs p, int tiles_m, int tiles_n) {
+template <int BM, int BN, bool TA, bool TB, int NWV = 4, int KG = 1>
+__global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_mfma(GemmArgs p, int tiles_m, int tiles_n) {
     constexpr int WGN = NWV / 2;  // waves along N (2 along M)
     constexpr int BK = MB_K, WM = BM / 2, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
     constexpr int A_EL = BM * BK, B_EL = BN * BK, STAGE = A_EL + B_EL;
-    constexpr int NST = mfma_stages<BM>();
+    constexpr int NST = KG > 1 ? 2 : mfma_stages<BM>();  // per K group
     constexpr int LPT = (BM * BK / 512 + BN * BK / 512) / NWV;  // DMA loads per wave per tile
     constexpr int OUT_LD = WN + 8;
     constexpr int OUT_EL = NWV * WM * OUT_LD;
-    constexpr int LDS_EL = OUT_EL > NST * STAGE ? OUT_EL : NST * STAGE;
+    constexpr int LDS_EL = OUT_EL > KG * NST * STAGE ? OUT_EL : KG * NST * STAGE;
+    static_assert(KG == 1 || (KG - 1) * NWV * FM * FN * 64 * 8 <= KG * NST * STAGE,
+                  "K-group partials fit in the stages");
     __shared__ __attribute__((aligned(1024))) f16 smem[LDS_EL];
 
     const int M = p.M, N = p.N, K = p.K;
@@ -336,7 +341,10 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_mfma(GemmArgs p, int tiles_m
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // KG > 1: KG groups of NWV waves; group kg takes the kg-th range of the
+    // K tiles in its own LDS stages, and the groups' fp32 sums meet in LDS
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kg = wave_all / NWV, wave = wave_all % NWV;
     const int l16 = lane & 15, g = lane >> 4;
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
     const int trow = l16 >> 2, tcol = (l16 & 3) * 4;
@@ -394,25 +402,49 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_mfma(GemmArgs p, int tiles_m
         });
     };
 
-    // tile kt lives in stage kt % NST; NST-1 tiles are in flight
-    const int KT = (K + BK - 1) / BK;
+    // tile kt of the group's range lives in stage kt % NST; NST-1 tiles are
+    // in flight.  Every group runs the same number of barrier steps.
+    const int KT_ALL = (K + BK - 1) / BK, per = (KT_ALL + KG - 1) / KG;
+    const int kt_base = kg * per, KT = max(0, min(KT_ALL - kt_base, per));
+    f16* gsm = smem + kg * NST * STAGE;
 #pragma unroll
     for (int t2 = 0; t2 < NST - 1; ++t2)
-        if (t2 < KT) issue(t2 * BK, smem + t2 * STAGE, smem + t2 * STAGE + A_EL);
-    for (int kt = 0; kt < KT; ++kt) {
+        if (t2 < KT) issue((kt_base + t2) * BK, gsm + t2 * STAGE, gsm + t2 * STAGE + A_EL);
+    for (int kt = 0; kt < per; ++kt) {
         // this wave's loads of tile kt are in LDS once at most the loads of
         // the younger tiles in flight remain (loads complete in order)
-        wait_vmcnt(LPT * min(NST - 2, KT - 1 - kt));
+        wait_vmcnt(LPT * max(0, min(NST - 2, KT - 1 - kt)));
         __syncthreads();  // everyone's; the stage of tile kt-1 is free again
         if (kt + NST - 1 < KT) {
-            f16* nxt = smem + ((kt + NST - 1) % NST) * STAGE;
-            issue((kt + NST - 1) * BK, nxt, nxt + A_EL);
+            f16* nxt = gsm + ((kt + NST - 1) % NST) * STAGE;
+            issue((kt_base + kt + NST - 1) * BK, nxt, nxt + A_EL);
         }
-        const f16* cur = smem + (kt % NST) * STAGE;
+        if (kt >= KT) continue;
+        const f16* cur = gsm + (kt % NST) * STAGE;
         compute(cur, cur + A_EL);
     }
 
+    if constexpr (KG > 1) {
+        // groups 1.. store their sums lane-major; group 0 adds them in group order
+        __syncthreads();  // every group is done with its stages
+        floatx4* red = reinterpret_cast<floatx4*>(smem);
+        if (kg > 0) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) red[((((kg - 1) * NWV + wave) * FM + i) * FN + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (kg == 0) {
+            for (int q = 1; q < KG; ++q)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] += red[((((q - 1) * NWV + wave) * FM + i) * FN + j) * 64 + lane];
+        }
+    }
     if (p.acc) {  // C += A B: one rounding of the fp32 sum per element
+        if (kg > 0) return;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -433,6 +465,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_mfma(GemmArgs p, int tiles_m
     // staging area overlaps the stages, which every wave has finished
     // reading once all have passed this barrier
     __syncthreads();
+    if (kg > 0) return;  // past the last barrier: group 0 stores the tile
     f16* ot = smem + wave * WM * OUT_LD;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -706,6 +739,14 @@ hipError_t launch_mfma(const GemmArgs& a, int batch, hipStream_t st) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
     dim3 grid((unsigned)(tm * tn), 1, batch);
     constexpr int NWV = (BM >= 256 && BN >= 256) ? 8 : 4;  // the large tile: two waves per SIMD
+    if constexpr (BM == 64) {
+        // at most one tile per CU and a long K: four K groups per workgroup
+        // (16 waves), so that four shorter load/compute chains overlap
+        if ((int64_t)tm * tn * batch <= device_cu_count() && a.K >= 16 * MB_K) {
+            hipLaunchKernelGGL((gemm_mfma<BM, BN, TA, TB, NWV, 4>), grid, dim3(64 * NWV * 4), 0, st, a, tm, tn);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((gemm_mfma<BM, BN, TA, TB, NWV>), grid, dim3(64 * NWV), 0, st, a, tm, tn);
     return hipGetLastError();
 }
