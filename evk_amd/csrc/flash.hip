@@ -715,6 +715,8 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     float* ob = smem_f;                          // [wave][ROWS][OW]
     float* mw = smem_f + 4 * ROWS * L::OW;       // [wave][ROWS]
     float* lw = mw + 4 * ROWS;                   // [wave][ROWS]
+    // wave w finishes the rows of its block qb = w; it stores the other
+    // blocks' partial state for the waves that finish them and keeps its own
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int q = qb * 16 + ml16;
@@ -722,41 +724,62 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             mw[wave * ROWS + q] = m_ref[qb];
             lw[wave * ROWS + q] = lacc[qb][0];
         }
+        if (qb != wave) {
 #pragma unroll
-        for (int d = 0; d < DB; ++d)
-            *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb];
+            for (int d = 0; d < DB; ++d)
+                *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb];
+        }
     }
     half_sync(8);
-    // wave w finishes rows [w*ROWS/4, (w+1)*ROWS/4): a lane owns 8 dh of one row
-    constexpr int CPR = DH / 8, RPW = ROWS / 4;
-    for (int rr = ml / CPR; rr < RPW; rr += 64 / CPR) {
-        const int q = wave * RPW + rr;
-        const int row = R0 + q;
-        const int dc = (ml % CPR) * 8;
-        float mv[4], m = -INFINITY;
+    static_assert(QB == 4, "one 16-row block per wave of the half");
+    // lane (mg, ml16): row q = 16 wave + ml16, dh 16 d + 4 mg + j
+    const int q = wave * 16 + ml16;
+    float mv[4], m = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            mv[w] = mw[w * ROWS + q];
-            m = fmaxf(m, mv[w]);
-        }
-        floatx4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        float l = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+        mv[w] = mw[w * ROWS + q];
+        m = fmaxf(m, mv[w]);
+    }
+    floatx4 a[DB];
+    float l = 0.0f;
+    auto own_block = [&](int w, floatx4 (&r)[DB]) {
+        // the wave's own block qb = wave, from registers (static indices)
+        static_for<QB>([&](auto qc) {
+            constexpr int qb = decltype(qc)::value;
+            if (w == qb) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float sc = mv[w] == -INFINITY ? 0.0f : fast_exp2(mv[w] - m);
-            l += sc * lw[w * ROWS + q];
-            a0 += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc);
-            a1 += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + dc + 4);
-        }
-        const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
-        if (active && row < NH) {
-            u32x4 o = {pack_h2(a0[0] * inv_l, a0[1] * inv_l), pack_h2(a0[2] * inv_l, a0[3] * inv_l),
-                       pack_h2(a1[0] * inv_l, a1[1] * inv_l), pack_h2(a1[2] * inv_l, a1[3] * inv_l)};
-            *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
-            if (p.lse && dc == 0) {
-                const float lse = l > 0.0f ? (m + log2f(l)) * kLn2 : -INFINITY;
-                p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
+                for (int d = 0; d < DB; ++d) r[d] = oacc[d][qb];
             }
+        });
+    };
+#pragma unroll
+    for (int d = 0; d < DB; ++d) a[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float sc = mv[w] == -INFINITY ? 0.0f : fast_exp2(mv[w] - m);
+        l += sc * lw[w * ROWS + q];
+        if (w == wave) {
+            floatx4 r[DB];
+            own_block(w, r);
+#pragma unroll
+            for (int d = 0; d < DB; ++d) a[d] += sc * r[d];
+        } else {
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                a[d] += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + d * 16 + mg * 4);
+        }
+    }
+    const int row = R0 + q;
+    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+    if (active && row < NH) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const uint2 o = {pack_h2(a[d][0] * inv_l, a[d][1] * inv_l), pack_h2(a[d][2] * inv_l, a[d][3] * inv_l)};
+            *reinterpret_cast<uint2*>(p.out + ((int64_t)b * NH + row) * DH + d * 16 + mg * 4) = o;
+        }
+        if (p.lse && mg == 0) {
+            const float lse = l > 0.0f ? (m + log2f(l)) * kLn2 : -INFINITY;
+            p.lse[((int64_t)b * H + row % H) * N + row / H] = lse;
         }
     }
 }

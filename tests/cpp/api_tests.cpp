@@ -749,9 +749,11 @@ static void test_graph_regression() {
 // Graph::causal_attention (fused causal flash attention) against the
 // reference's unfused matmul / mask / softmax / matmul composition on the
 // same inputs: output and the gradients of q, k and v.
-static void test_graph_causal_attention_fused_vs_unfused() {
-    std::printf("test_graph_causal_attention_fused_vs_unfused()\n");
-    const uint32_t B = 2, N = 48, D = 64;
+// Graph::causal_attention (flash forward + backward from the saved LSE)
+// against the reference's unfused chain (matmul, causal mask, softmax,
+// matmul; evk_ai.h:961-1007) on the same inputs and output gradient.
+static void test_graph_causal_attention_fused_vs_unfused(uint32_t B, uint32_t N, uint32_t D) {
+    std::printf("test_graph_causal_attention_fused_vs_unfused(B=%u, N=%u, D=%u)\n", B, N, D);
     Graph fused, plain;
     std::vector<float> qv = random_vec(B * N * D, 91), kv = random_vec(B * N * D, 92), vv = random_vec(B * N * D, 93);
     std::vector<float> gv = random_vec(B * N * D, 94);
@@ -1008,7 +1010,10 @@ int main(int argc, char** argv) {
     test_greedy_sample();
     test_training_ops();
     test_graph_regression();
-    test_graph_causal_attention_fused_vs_unfused();
+    test_graph_causal_attention_fused_vs_unfused(2, 48, 64);
+    // the reference's training shape (example/main_llm.cpp:694-702: one
+    // head, D = 256, batch 16, 160 positions): the wide-head flash kernels
+    test_graph_causal_attention_fused_vs_unfused(16, 160, 256);
     test_graph_tiny_lm();
     test_kv_decoder_matches_full_recompute();
     test_timestamps();
