@@ -548,7 +548,10 @@ DEV void gemv_finish(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
 
 template <int MR>
 __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ part, unsigned* cnt) {
-    __shared__ __attribute__((aligned(16))) float hv[SK_KC * MR];
+    // A's slice in LDS as fp16 pairs: pair P = rg + 32 v (v < SK_LD / 2) holds
+    // k = rg + 64 v and k + 32 of the K range for each row m, the two B rows
+    // that thread row group rg loads as its loads 2v and 2v+1
+    __shared__ __attribute__((aligned(16))) uint32_t hv[(SK_KC / 2) * MR];
     __shared__ float red[SK_RG * 4 * SK_CB];
     const int M = p.M, N = p.N, K = p.K;
     const int bz = blockIdx.z, ks = blockIdx.y, nks = gridDim.y;
@@ -573,23 +576,26 @@ __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ p
     }
     asm volatile("" ::: "memory");
     const __amdgpu_buffer_rsrc_t bres = buf_rsrc(B, (uint32_t)((int64_t)K * N * 2));
-    half8 w[SK_LD];
+    u32x4 w[SK_LD];
 #pragma unroll
     for (int u = 0; u < SK_LD; ++u) {
         const int i = r_lo + rg + u * SK_RG;
-        w[u] = as_half8(buf_load16(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0));
+        w[u] = buf_load16(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0);
     }
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int u = 0; u < APER; ++u) asm volatile("" : "+v"(av[u]));
-    // A into LDS as hv[k][m] (K-tail chunks were zero-filled by the loads)
+    // A into LDS pairs (K-tail chunks were zero-filled by the loads): the 8
+    // k of a chunk share v and h and have consecutive rg
+    f16* hvh = reinterpret_cast<f16*>(hv);
 #pragma unroll
     for (int u = 0; u < APER; ++u) {
         const int c = threadIdx.x + 256 * u, m = c / (SK_KC / 8), kk = (c % (SK_KC / 8)) * 8;
         if (c < ACH) {
             const half8 h = as_half8(av[u]);
+            const int hh = (kk >> 5) & 1, P0 = (kk & 31) + 32 * (kk >> 6);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hv[(kk + e) * MR + m] = (float)h[e];
+            for (int e = 0; e < 8; ++e) hvh[((P0 + e) * MR + m) * 2 + hh] = h[e];
         }
     }
     __syncthreads();
@@ -599,17 +605,26 @@ __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ p
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
+    // two B rows at a time: the column pairs (row k, row k + 32) go through
+    // v_dot2_f32_f16 against A's pair (fp32 accumulation, no conversions)
 #pragma unroll
-    for (int u = 0; u < SK_LD; ++u) {
-        const float* hr = hv + (rg + u * SK_RG) * MR;  // zeros past K
-        float hm[MR];
+    for (int v = 0; v < SK_LD / 2; ++v) {
+        const uint32_t* hr = hv + (rg + 32 * v) * MR;  // zeros past K
+        uint32_t a2[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) hm[m] = hr[m];
+        for (int m = 0; m < MR; ++m) a2[m] = hr[m];
+        const u32x4 w0 = w[2 * v], w1 = w[2 * v + 1];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float wv = (float)w[u][e];
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t blo = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);  // column 2d
+            const uint32_t bhi = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);  // column 2d + 1
 #pragma unroll
-            for (int m = 0; m < MR; ++m) acc[m][e] += hm[m] * wv;
+            for (int m = 0; m < MR; ++m) {
+                acc[m][2 * d] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a2[m]),
+                                                       __builtin_bit_cast(half2_t, blo), acc[m][2 * d], false);
+                acc[m][2 * d + 1] = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a2[m]),
+                                                           __builtin_bit_cast(half2_t, bhi), acc[m][2 * d + 1], false);
+            }
         }
     }
 
