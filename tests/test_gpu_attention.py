@@ -318,6 +318,28 @@ def test_kv_cache_write(dev, orc):
         assert np.array_equal(from_dev(C), want)
 
 
+@pytest.mark.parametrize("D,H", [(256, 1), (96, 2)])
+def test_wide_head_long_sequence(dev, orc, D, H):
+    """The head-256 / head-96 MFMA kernels over a long causal sequence (1024
+    positions: many key tiles per row block and many row tiles per key
+    block), forward with LSE and backward, against the oracle."""
+    import evk_amd as evk
+    B, N = 1, 1024
+    q = orc.normal_f16((B, N, H * D), 291 + D)
+    k = orc.normal_f16((B, N, D), 292 + D)
+    v = orc.normal_f16((B, N, D), 293 + D)
+    g = orc.normal_f16((B, N, H * D), 294 + D)
+    o, lse = fwd(evk, dev, q, k, v, True)
+    wo, wl = orc.attention_fwd(q, k, v, True)
+    assert_close_f16(o, wo, what=f"O D={D}")
+    assert np.abs(lse - wl).max() < 1e-2
+    dq, dk, dv = bwd(evk, dev, q, k, v, g, True, True)
+    wq, wk, wv = orc.attention_bwd(q, k, v, g, True)
+    assert_close_f16(dq, wq, what=f"dQ D={D}")
+    assert_close_f16(dk, wk, what=f"dK D={D}")
+    assert_close_f16(dv, wv, what=f"dV D={D}")
+
+
 @pytest.mark.parametrize("use_lse", [True, False])
 def test_reference_training_shape_d256(dev, orc, use_lse):
     """The shape the reference trains with: Graph::causal_attention over one
