@@ -73,6 +73,31 @@ def test_large_tile_paths(dev, orc, M, N, K):
     assert_close_f16(got, orc.matmul(a, b), what=f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+def test_k_groups_ragged(dev, orc, ta, tb):
+    """Grids that fit the CUs once with a long K (64x64 tiles, K >= 1024) run
+    four K groups per workgroup whose sums meet in LDS: ragged M, N and a K
+    that is not a multiple of the 64-deep tile (the last group's range is
+    shorter), every operand order."""
+    import evk_amd as evk
+    M, N, K = 200, 136, 1096
+    a = orc.uniform_f16((K, M) if ta else (M, K), 61 + ta)
+    b = orc.uniform_f16((N, K) if tb else (K, N), 62 + tb)
+    got = run_mm(evk, dev, a, b, (M, N), ta, tb)
+    assert_close_f16(got, orc.matmul(a, b, transpose_a=ta, transpose_b=tb), what=f"K groups {ta}{tb}")
+
+
+def test_k_groups_batched_acc(dev, orc):
+    """K groups with accumulation into C (one rounding of the fp32 sum per
+    element) over a batch."""
+    import evk_amd as evk
+    a = orc.uniform_f16((3, 96, 2056), 63)
+    b = orc.uniform_f16((2056, 72), 64)
+    c0 = orc.uniform_f16((3, 96, 72), 65)
+    got = run_mm(evk, dev, a, b, None, acc=True, c0=c0)
+    assert_close_f16(got, orc.matmul(a, b, c=c0, acc_c=True), what="K groups batched acc")
+
+
 def test_batched_broadcast_acc(dev, orc):
     import evk_amd as evk
     a = orc.uniform_f16((3, 96, 80), 51)
