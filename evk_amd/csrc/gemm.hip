@@ -580,7 +580,8 @@ __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ p
 #pragma unroll
     for (int u = 0; u < SK_LD; ++u) {
         const int i = r_lo + rg + u * SK_RG;
-        w[u] = buf_load16(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0);
+        // nontemporal: B is read once (the MFMA kernel below measured slower with it)
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(bres, oob_or(col_ok && i < r_hi, (uint32_t)(((int64_t)i * N + col) * 2)), 0, 2);
     }
     asm volatile("" ::: "memory");
 #pragma unroll

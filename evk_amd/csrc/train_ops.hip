@@ -32,9 +32,18 @@ constexpr int EW_NT = 256;  // threads of an elementwise workgroup
 DEV float hf(f16 x) { return (float)x; }
 
 // 8 consecutive fp16 values at p[i0..i0+8) (fewer at the tail) as floats
+// Streaming accesses: nontemporal loads and stores for data that a kernel
+// reads or writes once (elementwise ops, Adam: 65 -> 77 % of HBM; the
+// cross-entropy rows: 66 -> 71 %; the register softmax measured slower)
+DEV half8 ld_stream(const half8* p) {
+    return __builtin_bit_cast(half8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
+DEV void st_stream(half8* p, const half8& v) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+}
 DEV void ld8(const f16* p, int64_t i0, int64_t n, bool vec, float (&v)[8]) {
     if (vec && i0 + 8 <= n) {
-        const half8 h = *reinterpret_cast<const half8*>(p + i0);
+        const half8 h = ld_stream(reinterpret_cast<const half8*>(p + i0));
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
     } else {
@@ -47,7 +56,7 @@ DEV void st8(f16* p, int64_t i0, int64_t n, bool vec, const float (&v)[8]) {
         half8 h;
 #pragma unroll
         for (int e = 0; e < 8; ++e) h[e] = (f16)v[e];
-        *reinterpret_cast<half8*>(p + i0) = h;
+        st_stream(reinterpret_cast<half8*>(p + i0), h);
     } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -504,7 +513,7 @@ __global__ __launch_bounds__(NT) void ce_row_reg_k(const f16* logits, const uint
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int c = threadIdx.x + CE_NT * u;
-        if (c < nc) r[u] = x[c];
+        if (c < nc) r[u] = ld_stream(x + c);
     }
     auto cl = [](f16 h) { return fminf(fmaxf((float)h, -65000.0f), 65000.0f); };
     float mx = -3.402823466e+38f;
@@ -552,7 +561,7 @@ __global__ __launch_bounds__(NT) void ce_row_reg_k(const f16* logits, const uint
                     ws[1 + row] = ((mx + log_sum) - xv) * inv_valid;
                 }
         }
-        g[c] = o;
+        st_stream(g + c, o);
     }
 }
 
