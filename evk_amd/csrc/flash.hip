@@ -1113,8 +1113,9 @@ DEV void bwd_kv_body(const FlashArgs& p, float* part_ws, int parts_per_batch, in
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
-            mine[((0 * 2 + k2) * DB + d) * 64 + lane] = dk[k2][d];
-            mine[((1 * 2 + k2) * DB + d) * 64 + lane] = dv[k2][d];
+            // nontemporal: written once here, read once by the reduce kernel
+            __builtin_nontemporal_store(dk[k2][d], mine + ((0 * 2 + k2) * DB + d) * 64 + lane);
+            __builtin_nontemporal_store(dv[k2][d], mine + ((1 * 2 + k2) * DB + d) * 64 + lane);
         }
 }
 
@@ -1141,7 +1142,7 @@ __global__ __launch_bounds__(256) void flash_bwd_kv_reduce(FlashArgs p, const fl
             floatx4 v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u)
-                if (q + u < nparts) v[u] = src[(int64_t)(q + u) * SLOT];
+                if (q + u < nparts) v[u] = __builtin_nontemporal_load(src + (int64_t)(q + u) * SLOT);
             if (q == 0) acc = v[0];
             else acc += v[0];
 #pragma unroll
@@ -1343,7 +1344,7 @@ DEV void bwd_q_body(const FlashArgs& p, int blk, char* lds) {
             const float sc = p.scale;
             u32x4 o = {pack_h2(a0[0] * sc, a0[1] * sc), pack_h2(a0[2] * sc, a0[3] * sc),
                        pack_h2(a1[0] * sc, a1[1] * sc), pack_h2(a1[2] * sc, a1[3] * sc)};
-            *reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc) = o;
+            __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(p.out + ((int64_t)b * NH + row) * DH + dc));
         }
     }
 }
