@@ -481,7 +481,8 @@ __global__ __launch_bounds__(64 * NWV * KG, 1) void gemm_mfma(GemmArgs p, int ti
         const int r = q / CPR, cc = (q % CPR) * 8;
         const int row = m0 + wm0 + r, col = n0 + wn0 + cc;
         const u32x4 v = *reinterpret_cast<const u32x4*>(ot + r * OUT_LD + cc);
-        if (row < M && col < N) *reinterpret_cast<u32x4*>(Cp + (int64_t)row * N + col) = v;
+        // nontemporal: C is written once (QKV shape 0.785 -> 0.763 ms)
+        if (row < M && col < N) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(Cp + (int64_t)row * N + col));
     }
 }
 
