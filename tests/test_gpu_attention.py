@@ -125,6 +125,24 @@ def test_config3_causal_flash_backward(dev, orc, use_lse):
     assert_close_f16(dv, wv, what="dV")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_backward_dh32_split_parts(dev, orc, causal):
+    """Head size 32 over enough query rows (1000 positions x 4 heads) that
+    the key blocks' rows are split into several parts, whose fp32 partials
+    the reduce kernel sums; the last key block is ragged (1000 keys)."""
+    import evk_amd as evk
+    B, H, S, Dh = 2, 4, 1000, 32
+    q = orc.normal_f16((B, S, H * Dh), 301)
+    k = orc.normal_f16((B, S, Dh), 302)
+    v = orc.normal_f16((B, S, Dh), 303)
+    g = orc.normal_f16((B, S, H * Dh), 304)
+    dq, dk, dv = bwd(evk, dev, q, k, v, g, causal, True)
+    wq, wk, wv = orc.attention_bwd(q, k, v, g, causal)
+    assert_close_f16(dq, wq, what=f"dQ dh32 causal={causal}")
+    assert_close_f16(dk, wk, what=f"dK dh32 causal={causal}")
+    assert_close_f16(dv, wv, what=f"dV dh32 causal={causal}")
+
+
 @pytest.mark.parametrize("Dh", [32, 64, 128, 16, 48, 96, 256])
 @pytest.mark.parametrize("N", [16, 45, 96])
 def test_flash_backward_ragged(dev, orc, Dh, N):
