@@ -36,7 +36,7 @@ METRIC = "fp16 GEMM & flash-attn fwd/bwd TFLOP/s (% MFMA peak); decode tok/s, GB
 # --only names, one workload each (profiling runs take one at a time so that
 # a kernel-trace summary never mixes shapes under one kernel name)
 WORKLOADS = ["flash_fwd", "gemm_1024", "gemm_4096", "gemm_qkv", "gemv_m1", "gemv_m4", "gemv_m16", "flash_bwd",
-             "decode", "train_adam", "train_ce", "train_softmax", "graph_attn"]
+             "decode", "kv_decoder", "train_adam", "train_ce", "train_softmax", "graph_attn"]
 
 
 def parse():
@@ -382,6 +382,20 @@ def main():
                             "kernel_per_stage_path_ms_per_token": round(ms32_k / 32, 4),
                             "prefill_1024_tokens_ms": round(ms_pre, 4)}
         del w, cache, packed
+    if want("kv_decoder"):
+        # the reference caller's sampling loop (example/main_llm.cpp:622-654,
+        # B=16, D=256, 8 layers, vocab 144, positions 18..107) through
+        # evk::ai::KVCacheDecoder against the Graph's full recompute per
+        # position; a C++ program over the evk::ai API, run as a child process
+        import subprocess
+        exe = os.path.join(ROOT, "evk_amd", "bin", "kv_decoder_tool")
+        torch.cuda.synchronize()
+        r = subprocess.run([exe, "bench", "3"], capture_output=True, text=True, timeout=300)
+        line = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else ""
+        if r.returncode == 0 and line.startswith("{"):
+            sec["kv_decoder_main_llm"] = json.loads(line)
+        else:
+            print(f"bench.py: kv_decoder_tool failed (rc {r.returncode}): {r.stderr[-500:]}", file=sys.stderr)
     if want("train_adam"):
         # training ops (HBM-bound)
         n_p = 64 << 20
@@ -456,6 +470,10 @@ def main():
             del qa, ka, va, ga, oa, dqa, dka, dva, sc_, pr_, dp_, ds_, ou_, dqu, dku, dvu
     if sec:
         out["secondary"] = sec
+    # release the library's device workspaces (decode mailboxes, flash and
+    # GEMV partials) while the runtime is fully up, not in exit handlers
+    torch.cuda.synchronize()
+    evk.shutdown()
 
     # ---------------- CPU baseline (the oracle's C restatement) -----------
     if not args.no_cpu:

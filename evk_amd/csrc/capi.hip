@@ -194,6 +194,13 @@ static int flash_shapes(const evkhip_tensor* q, const evkhip_tensor* k, const ev
 
 int evkhip_flash_has_mfma(uint32_t head_dim) { return flash_mfma_head(head_dim) ? 1 : 0; }
 
+int evkhip_flash_kernel_path(uint32_t n, uint32_t heads, uint32_t head_dim) {
+    if (head_dim == 0 || heads == 0 || !flash_mfma_head(head_dim)) return EVKHIP_FLASH_PATH_SCALAR;
+    if (flash_wide_head(head_dim))
+        return flash_wide_fits(n, heads, head_dim) ? EVKHIP_FLASH_PATH_WIDE : EVKHIP_FLASH_PATH_SCALAR;
+    return EVKHIP_FLASH_PATH_MFMA;
+}
+
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k, const evkhip_tensor* v,
                            const evkhip_tensor* o, int causal, float* lse, void* stream) {
     uint32_t B, N, D, Dh;

@@ -1,5 +1,5 @@
 // Persistent greedy decode: every stage of every decode step in one
-// cooperative launch (the decode loop of the reference's caller,
+// persistent launch (the decode loop of the reference's caller,
 // example/main_llm.cpp:622-654, in the KV-cached form of model.hip).
 //
 // Why: a decode step of the C4 model is 61 dependent matrix-vector stages
@@ -504,16 +504,19 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             }
         }
         __syncthreads();
-        if (s_fail) {
-            fail();
-            return;
-        }
         base = 0u;
     }
+    // every workgroup arrives, also one that gave up at the wrap barrier:
+    // a partial count would make the first arrival of a later launch look
+    // like the last one
     if (threadIdx.x == 0 &&
         __hip_atomic_fetch_add(&a.ctl[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1u) {
         __hip_atomic_store(&a.ctl[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&a.ctl[0], base + need, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (s_fail) {
+        fail();
+        return;
     }
     auto tag_of = [&](int t, int k) { return base + 1u + (uint32_t)t * (uint32_t)SPT + (uint32_t)k; };
     const int HEAD = 5 * a.L;
@@ -1231,9 +1234,15 @@ int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, 
     a.G3 = pl.G3; a.R3 = pl.R3; a.G5 = pl.G5; a.R5 = pl.R5;
     a.bufb = pl.bufb; a.hr = pl.hr;
     a.spin_limit = (int)std::min(flash_spin_limit(), 1u << 18);
-    void* args[] = {&a};
-    EVK_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_persist), dim3((unsigned)pl.G),
-                                       dim3(PNT), args, (unsigned)pl.lds, st));
+    // An ordinary launch: the occupancy check above keeps all G workgroups
+    // resident at once (one per CU), and every in-kernel wait is bounded, so
+    // a workgroup that is held back (another stream's kernel on its CU)
+    // delays the others or, at worst, ends the launch with
+    // EVKHIP_STATUS_WAIT_TIMEOUT.  The cooperative launch API is not used:
+    // the runtime state it creates was torn down after the profiler's own
+    // finalisation at process exit and crashed rocprofv3 runs there.
+    hipLaunchKernelGGL(decode_persist, dim3((unsigned)pl.G), dim3(PNT), (unsigned)pl.lds, st, a);
+    EVK_HIP(hipGetLastError());
     return EVKHIP_OK;
 }
 

@@ -1881,7 +1881,7 @@ int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) {
     if (mfma && dh == 32) e = launch_fwd<32>(a, causal, 0, st);
     else if (mfma && dh == 64) e = launch_fwd<64>(a, causal, 0, st);
     else if (mfma && dh == 128) e = launch_fwd<128>(a, causal, 0, st);
-    else if (mfma && flash_wide_head(dh)) e = flash_forward_wide(a, dh, causal, st);
+    else if (mfma && flash_wide_head(dh) && flash_wide_fits(a.N, a.H, dh)) e = flash_forward_wide(a, dh, causal, st);
     else {
         dim3 g((unsigned)(((int64_t)a.B * a.N * a.H + 63) / 64));
         hipLaunchKernelGGL(flash_fwd_scalar, g, dim3(64), 0, st, a, dh, (int)causal, 0);
@@ -1897,7 +1897,7 @@ int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st) 
     const size_t rows = (size_t)a.B * a.N * a.H;
     const bool have_lse = a.lse != nullptr;
     const bool split = mfma && dh <= 64 && !flash_wide_head(dh) && (int64_t)a.N * a.H * dh * 2 < (int64_t)INT32_MAX;
-    const bool wide = mfma && flash_wide_head(dh);
+    const bool wide = mfma && flash_wide_head(dh) && flash_wide_fits(a.N, a.H, dh);
     // arena layout (256-byte aligned pieces)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const int nkb = (a.N + BKB - 1) / BKB;

@@ -55,6 +55,11 @@ hipError_t flash_forward_wide(const FlashArgs& a, int dh, bool causal, hipStream
 hipError_t flash_backward_wide(const FlashArgs& a, int dh, bool causal, hipStream_t st);
 // Head sizes with MFMA forward and backward kernels.
 inline bool flash_mfma_head(uint32_t dh) { return dh == 32 || dh == 64 || dh == 128 || flash_wide_head(dh); }
+// The wide-head kernels address one batch of Q (and dO, O) through 32-bit
+// buffer offsets: they run only while that batch stays below 2 GiB.
+inline bool flash_wide_fits(uint64_t N, uint64_t H, uint32_t dh) {
+    return N * H * dh * 2u < (uint64_t)INT32_MAX;
+}
 int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 void flash_free_workspace();

@@ -106,7 +106,8 @@ int evkhip_matmul_noalloc(const evkhip_tensor* a, const evkhip_tensor* b, const 
  * MQA: Q,O (B,N,H*Dh); K,V (B,N,Dh); H = D/Dh; scale 1/sqrt(Dh).
  * Extensions (defaults reproduce the reference): causal != 0 masks keys
  * j > i; lse, if non-NULL, receives the fp32 log-sum-exp of every (b,h,i)
- * row, laid out (B,H,N).  Dh in {16,32,64,128}. */
+ * row, laid out (B,H,N).  Dh up to 256: multiples of 16 run MFMA kernels
+ * (evkhip_flash_kernel_path), other sizes a scalar kernel. */
 int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k,
                            const evkhip_tensor* v, const evkhip_tensor* o,
                            int causal, float* lse, void* stream);
@@ -114,6 +115,17 @@ int evkhip_flash_attention(const evkhip_tensor* q, const evkhip_tensor* k,
 /* Non-zero when the flash forward and backward run MFMA kernels for this
  * head size (no reference counterpart); other sizes take a scalar path. */
 int evkhip_flash_has_mfma(uint32_t head_dim);
+
+/* Which kernel family serves flash attention (forward and backward) at N
+ * positions, `heads` query heads of head_dim (no reference counterpart; a
+ * host-side query, no GPU work): MFMA kernels for 32, 64 and 128, the wide
+ * MFMA kernels for the other multiples of 16 up to 256 while one batch of Q
+ * stays below 2 GiB, the scalar kernels otherwise (pointers that are not
+ * 16-byte aligned also take the scalar kernels). */
+#define EVKHIP_FLASH_PATH_SCALAR 0
+#define EVKHIP_FLASH_PATH_MFMA 1
+#define EVKHIP_FLASH_PATH_WIDE 2
+int evkhip_flash_kernel_path(uint32_t n, uint32_t heads, uint32_t head_dim);
 
 /* evk::ai::flash_attention_bwd (evk_ai.h:503, evk_ai.cpp:371-473).
  * dQ (B,N,D); dK,dV (B,N,Dh) summed over the H heads sharing them.
@@ -321,8 +333,8 @@ int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* 
  * (vocab,d)); evkhip_model_packed_elems elements, the same count.  Pack once
  * per weight set (and again after the weights change).
  * evkhip_model_decode_packed then has the meaning of evkhip_model_decode but
- * runs all n_steps in one cooperative launch whose stages hand their outputs
- * over in device memory.  It needs d and hidden multiples of 8 (at most 8192
+ * runs all n_steps in one persistent launch (one workgroup per CU, all
+ * resident at once) whose stages hand their outputs over in device memory.  It needs d and hidden multiples of 8 (at most 8192
  * each), dh in {16,32,64,128}, max_seq <= 8192, heads * ceil(max_seq / 128)
  * <= 144 and no more than the workgroups it runs (one per CU), and
  * per-workgroup weight slices that fit in LDS (d=768, hidden=3072 do); other

@@ -134,6 +134,27 @@ def test_flash_validation(L):
                                     b(T((0, 16, 128))), 1, None, None) == OK
 
 
+def test_flash_kernel_path(L):
+    """The wide-head MFMA kernels address one batch of Q through 32-bit buffer
+    offsets: at 2 GiB and above the dispatch takes the scalar kernels."""
+    SCALAR, MFMA, WIDE = 0, 1, 2
+    for dh in (32, 64, 128):
+        assert L.evkhip_flash_kernel_path(1024, 8, dh) == MFMA
+    for dh in (16, 48, 80, 96, 160, 256):
+        assert L.evkhip_flash_kernel_path(1024, 8, dh) == WIDE
+    for dh in (8, 24, 100, 0):
+        assert L.evkhip_flash_kernel_path(1024, 8, dh) == SCALAR
+    # N * H * dh * 2 bytes against INT32_MAX
+    lim = (2**31 - 1)
+    n = lim // (2 * 256)  # 4194303 rows of head 256: just below
+    assert n * 256 * 2 < lim
+    assert L.evkhip_flash_kernel_path(n, 1, 256) == WIDE
+    assert L.evkhip_flash_kernel_path(n + 1, 1, 256) == SCALAR
+    assert L.evkhip_flash_kernel_path(1 << 22, 8, 48) == SCALAR  # 3.2 GB of Q per batch
+    assert L.evkhip_flash_kernel_path(1 << 22, 1, 48) == WIDE    # 403 MB
+    assert L.evkhip_flash_kernel_path(1 << 30, 1, 64) == MFMA  # these pick a sub-kernel by size themselves
+
+
 def test_decode_op_validation(L):
     b = C.byref
     q, kc = T((768,)), T((1056, 768))

@@ -313,8 +313,8 @@ def test_decode_packed_repeated_and_replayed(dev, orc):
     try:
         with torch.cuda.graph(g):
             run()
-    except Exception as ex:  # cooperative launches not capturable here
-        pytest.skip(f"graph capture of the cooperative launch failed: {ex}")
+    except Exception as ex:
+        pytest.fail(f"graph capture of the persistent launch failed: {ex}")
     for _ in range(2):
         tok.zero_()
         g.replay()
