@@ -72,13 +72,19 @@ def build(verbose: bool = False) -> None:
              ["-L", HERE, "-levkhip", "-Wl,-rpath,$ORIGIN"])
         os.replace(tmp, lib)
     if api:
-        # the evk / evk::ai API tests (tests/cpp), linked against libevk.so
+        # programs over the evk / evk::ai API (tests/cpp), linked against
+        # libevk.so: the API tests and the main_llm decode tool
         os.makedirs(os.path.join(HERE, "bin"), exist_ok=True)
-        exe = os.path.join(HERE, "bin", "api_tests")
-        _run([HIPCC, "-x", "hip", "--offload-arch=" + ARCH] + HIP_FLAGS[1:] +
-             [os.path.join(ROOT, "tests", "cpp", "api_tests.cpp"), "-o", exe + ".tmp",
-              "-L", HERE, "-levk", "-levkhip", "-Wl,-rpath,$ORIGIN/.."])
-        os.replace(exe + ".tmp", exe)
+
+        def program(name):
+            exe = os.path.join(HERE, "bin", name)
+            _run([HIPCC, "-x", "hip", "--offload-arch=" + ARCH] + HIP_FLAGS[1:] +
+                 [os.path.join(ROOT, "tests", "cpp", name + ".cpp"), "-o", exe + ".tmp",
+                  "-L", HERE, "-levk", "-levkhip", "-Wl,-rpath,$ORIGIN/.."])
+            os.replace(exe + ".tmp", exe)
+
+        with cf.ThreadPoolExecutor(max_workers=2) as ex:
+            list(ex.map(program, ["api_tests", "kv_decoder_tool"]))
     if verbose:
         print("built", kern)
 

@@ -16,7 +16,7 @@ namespace {
 // ---------------------------------------------------------------------------
 // Single-query attention.  Grid (heads, nsplit); 256 threads.  A workgroup
 // covers cache rows [split*chunk, +chunk) of one head: LPK = DH/8 lanes per
-// key (16 bytes each), 256/LPK keys per pass.  Partial (m, l, o) go to
+// key (16 bytes each), 256/LPK keys per pass (DH = 256: 32 lanes, 8 keys).  Partial (m, l, o) go to
 // workspace; the last workgroup of a head merges the splits in split order.
 // ---------------------------------------------------------------------------
 struct SqArgs {
@@ -346,12 +346,12 @@ int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, in
     // from here on `heads` counts (sequence, head) pairs: one grid row each
     heads *= batch;
     a.scale_log2 = (1.0f / sqrtf((float)dh)) * kLog2e;
-    const bool vec = vec_ok && (dh == 16 || dh == 32 || dh == 64 || dh == 128) && (row_stride % 8 == 0);
+    const bool vec = vec_ok && (dh == 16 || dh == 32 || dh == 64 || dh == 128 || dh == 256) && (row_stride % 8 == 0);
     if (!vec) {
         size_t shm = sizeof(float) * ((size_t)L + dh);
         if (shm > 64 * 1024)
             return set_error(EVKHIP_ERR_UNSUPPORTED, "single_query_attention: head size %d with %d cached rows "
-                             "needs the vector path (dh in {16,32,64,128})", dh, L);
+                             "needs the vector path (dh in {16,32,64,128,256})", dh, L);
         hipLaunchKernelGGL(sq_attention_scalar, dim3(heads), dim3(256), shm, st, a, dh);
         hipError_t e = hipGetLastError();
         return e == hipSuccess ? EVKHIP_OK : check_hip(e, "sq_attention_scalar launch");
@@ -394,7 +394,8 @@ int sq_attention_launch(const f16* q, const f16* kc, const f16* vc, f16* out, in
         case 16: hipLaunchKernelGGL(sq_attention<16>, grid, dim3(256), 0, st, a); break;
         case 32: hipLaunchKernelGGL(sq_attention<32>, grid, dim3(256), 0, st, a); break;
         case 64: hipLaunchKernelGGL(sq_attention<64>, grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL(sq_attention<128>, grid, dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(sq_attention<128>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(sq_attention<256>, grid, dim3(256), 0, st, a); break;
     }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? EVKHIP_OK : check_hip(e, "sq_attention launch");

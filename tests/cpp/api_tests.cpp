@@ -929,7 +929,7 @@ static void test_kv_decoder_matches_full_recompute() {
                 mismatches, ties, max_dlogit);
     TEST(dec.cached() == PREFIX - 1 + STEPS);
     TEST(mismatches == 0);
-    TEST(max_dlogit < 3e-2f);
+    TEST(max_dlogit < 1e-2f);
 }
 
 static void test_timestamps() {

@@ -35,7 +35,7 @@ def test_config2_causal_flash_forward(dev, orc, causal):
     o, lse = fwd(evk, dev, q, k, v, causal)
     wo, wl = orc.attention_fwd(q, k, v, causal)
     assert_close_f16(o, wo, what="O")
-    assert np.abs(lse - wl).max() < 1e-2
+    assert np.abs(lse - wl).max() < 1e-3
 
 
 @pytest.mark.parametrize("Dh", [32, 64, 128, 16, 48, 96, 256])
@@ -50,7 +50,7 @@ def test_flash_forward_ragged_heads(dev, orc, Dh, N):
         o, lse = fwd(evk, dev, q, k, v, causal)
         wo, wl = orc.attention_fwd(q, k, v, causal)
         assert_close_f16(o, wo, what=f"O Dh={Dh} N={N} causal={causal}")
-        assert np.abs(lse - wl).max() < 1e-2
+        assert np.abs(lse - wl).max() < 1e-3
 
 
 @pytest.mark.parametrize("order", ["growing", "shrinking"])
@@ -70,7 +70,7 @@ def test_flash_forward_moving_maximum(dev, orc, order):
         o, lse = fwd(evk, dev, q, k, v, causal)
         wo, wl = orc.attention_fwd(q, k, v, causal)
         assert_close_f16(o, wo, what=f"O {order} causal={causal}")
-        assert np.abs(lse - wl).max() < 1e-2 * max(1.0, np.abs(wl).max() / 100)
+        assert np.abs(lse - wl).max() < 1e-3 * max(1.0, np.abs(wl).max() / 100)
 
 
 def test_flash_forward_row_sums(dev, orc):
@@ -228,7 +228,7 @@ def test_sq_attention_config4(dev, orc, L):
 
 def test_sq_attention_other_heads(dev, orc):
     import evk_amd as evk
-    for heads, dh, L in [(4, 128, 700), (8, 16, 300), (2, 48, 90), (3, 32, 1)]:
+    for heads, dh, L in [(4, 128, 700), (8, 16, 300), (2, 48, 90), (3, 32, 1), (1, 256, 1000), (2, 256, 65)]:
         q = orc.normal_f16((heads * dh,), 261 + dh)
         kc = orc.normal_f16((1024, heads * dh), 262)
         vc = orc.normal_f16((1024, heads * dh), 263)
@@ -350,7 +350,7 @@ def test_wide_head_long_sequence(dev, orc, D, H):
     o, lse = fwd(evk, dev, q, k, v, True)
     wo, wl = orc.attention_fwd(q, k, v, True)
     assert_close_f16(o, wo, what=f"O D={D}")
-    assert np.abs(lse - wl).max() < 1e-2
+    assert np.abs(lse - wl).max() < 1e-3
     dq, dk, dv = bwd(evk, dev, q, k, v, g, True, True)
     wq, wk, wv = orc.attention_bwd(q, k, v, g, True)
     assert_close_f16(dq, wq, what=f"dQ D={D}")
@@ -374,7 +374,7 @@ def test_reference_training_shape_d256(dev, orc, use_lse):
     o, lse = fwd(evk, dev, q, k, v, True)
     wo, wl = orc.attention_fwd(q, k, v, True)
     assert_close_f16(o, wo, what="O d256")
-    assert np.abs(lse - wl).max() < 1e-2
+    assert np.abs(lse - wl).max() < 1e-3
     dq, dk, dv = bwd(evk, dev, q, k, v, g, True, use_lse)
     wq, wk, wv = orc.attention_bwd(q, k, v, g, True)
     assert_close_f16(dq, wq, what="dQ d256")
