@@ -67,18 +67,24 @@ def profile_copy():
     print(f"copied {n} bytes x 20")
 
 
-def timed(fn, steps, warmup, check=None):
+REPLAYS = 5  # timed replays of the captured steps; the median is reported
+
+
+def timed(fn, steps, warmup, check=None, spread=None):
     """Average ms per call of fn() over exactly `steps` back-to-back calls.
 
     After `warmup` eager calls, the `steps` calls are captured into one HIP
     graph (torch.cuda.CUDAGraph: the library launches on torch's current
-    stream, which is the capture stream during capture) and the graph is
-    replayed once between two HIP events on the current stream, so that the
-    timed region holds the kernels without host launch gaps.  `check`
-    returns the output tensors; those of the replay must equal those of the
-    last eager call bit for bit (the kernels are deterministic), else the
-    eager launches are timed instead.  Capture failures also fall back to
-    eager launches."""
+    stream, which is the capture stream during capture).  The graph is
+    replayed once untimed, then REPLAYS times, each replay between two HIP
+    events on the current stream, so that the timed region holds the
+    kernels without host launch gaps; the median replay gives the figure
+    (steady state: the first replay after capture runs measurably slower).
+    If `spread` is a dict it receives the min and max over the replays.
+    `check` returns the output tensors; those of the replays must equal
+    those of the last eager call bit for bit (the kernels are
+    deterministic), else the eager launches are timed instead.  Capture
+    failures also fall back to eager launches."""
     import torch
     for _ in range(warmup):
         fn()
@@ -108,14 +114,36 @@ def timed(fn, steps, warmup, check=None):
         torch.cuda.synchronize()
         return s.elapsed_time(e) / steps
 
-    ms = run()
+    def median_run():
+        run()  # untimed
+        res = sorted(run() for _ in range(REPLAYS))
+        if spread is not None:
+            spread["min"], spread["max"] = res[0], res[-1]
+        return res[len(res) // 2]
+
+    ms = median_run()
     if graph is not None and check is not None:
         if not all(torch.equal(a, b) for a, b in zip(check(), want)):
             print("bench.py: graph replay differs from the eager result; timing eager launches",
                   file=sys.stderr)
             graph = None
-            ms = run()
+            ms = median_run()
     return ms
+
+
+def per_launch(fn, n):
+    """Median, min and max ms of n single eager launches, each between two
+    HIP events (the spread of one kernel's duration within a run)."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    for s, e in ev:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) for s, e in ev)
+    return t[n // 2], t[0], t[-1]
 
 
 def read_traffic(name):
@@ -275,9 +303,10 @@ def main():
     L = torch.empty((B, H, S), dtype=torch.float32, device=dev)
     flops = 2.0 * B * H * S * S * Dh
     torch.cuda.synchronize()
+    head_spread = {}
     if want("flash_fwd"):
         ms = timed(lambda: evk.flash_attention(Q, K, V, O, causal=True, lse=L), args.steps, args.warmup,
-                   check=lambda: (O, L))
+                   check=lambda: (O, L), spread=head_spread)
         tflops = flops / (ms * 1e-3) / 1e12
     else:  # a profiling run of other workloads only
         ms, tflops = float("nan"), float("nan")
@@ -303,29 +332,38 @@ def main():
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic},
     }
+    if head_spread:
+        out["timing"] = {"replays": REPLAYS, "statistic": "median replay of the captured steps",
+                         "ms_per_step_min": round(head_spread["min"], 5),
+                         "ms_per_step_max": round(head_spread["max"], 5)}
 
     # ---------------- secondary configurations ---------------------------
     sec = {}
 
-    def gemm(gm, gn, gk, seed, steps):
+    def gemm(gm, gn, gk, seed, steps, launches=0):
         a = to_dev(orc.uniform_f16((gm, gk), seed))
         b = to_dev(orc.uniform_f16((gk, gn), seed + 1))
         c = torch.empty((gm, gn), dtype=torch.float16, device=dev)
         ms_ = timed(lambda: evk.matmul(a, b, c), steps, 5, check=lambda: (c,))
+        pl = per_launch(lambda: evk.matmul(a, b, c), launches) if launches else None
         del a, b, c
-        return ms_
+        return ms_, pl
 
     for key, name, (gm, gn, gk, st) in [("gemm_1024", "gemm_1024", (1024, 1024, 1024, 200)),
                                         ("gemm_4096", "gemm_4096", (4096, 4096, 4096, 30)),
                                         ("gemm_qkv", "gemm_qkv_8192x12288x4096", (8192, 12288, 4096, 10))]:
         if want(key):
-            ms_ = gemm(gm, gn, gk, 101, st)
+            ms_, pl = gemm(gm, gn, gk, 101, st, launches=0 if key == "gemm_1024" else 30)
             tf = 2.0 * gm * gn * gk / (ms_ * 1e-3) / 1e12
             sec[name] = {"ms": round(ms_, 4), "TFLOP/s": round(tf, 1),
                          "frac_mfma_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+            if pl:
+                # single eager launches between events: the kernel's own spread
+                sec[name]["per_launch_ms"] = {"median": round(pl[0], 4), "min": round(pl[1], 4),
+                                              "max": round(pl[2], 4), "launches": 30}
     for gm in (1, 4, 16):
         if want(f"gemv_m{gm}"):
-            ms_ = gemm(gm, 11008, 4096, 501, 200)
+            ms_, _ = gemm(gm, 11008, 4096, 501, 200)
             gbs = (4096 * 11008 + gm * 4096 + gm * 11008) * 2 / (ms_ * 1e-3) / 1e9
             sec[f"gemv_m{gm}_11008x4096"] = {"ms": round(ms_, 4), "GB/s": round(gbs, 1),
                                             "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}

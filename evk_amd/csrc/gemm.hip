@@ -547,6 +547,46 @@ DEV void gemv_finish(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
     }
 }
 
+// The same finish for up to 16 rows (the MFMA kernel): a thread's items
+// (m, column) are idx = tid + 256 u; every partial of all of them is
+// requested before any is added (one round trip to the coherence point
+// instead of one per item), then each item's partials are added in range
+// order, as in gemv_finish.
+DEV void gemv_finish_m16(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
+    const int M = p.M, N = p.N, bz = blockIdx.z, nks = gridDim.y;
+    if (!arrive_last(cnt + bz * gridDim.x + blockIdx.x, nks)) return;
+    f16* Cp = p.C + (int64_t)bz * p.sC;
+    const int64_t stride = (int64_t)M * N;
+    constexpr int IPT = 16 * SK_CB / 256;   // items per thread at M = 16
+    constexpr int PB = 8;                    // ranges per batch of loads
+    float v[IPT];
+#pragma unroll
+    for (int u = 0; u < IPT; ++u) v[u] = 0.0f;
+    for (int s0 = 0; s0 < nks; s0 += PB) {
+        float t[IPT][PB];
+#pragma unroll
+        for (int u = 0; u < IPT; ++u) {
+            const int idx = threadIdx.x + 256 * u, m = idx / SK_CB, gc = c0 + idx % SK_CB;
+            const bool ok = m < M && gc < N;
+            const float* src = part + ((int64_t)bz * nks * M + m) * N + gc;
+#pragma unroll
+            for (int s = 0; s < PB; ++s) t[u][s] = (ok && s0 + s < nks) ? ld_ag(src + (s0 + s) * stride) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < IPT; ++u)
+#pragma unroll
+            for (int s = 0; s < PB; ++s) v[u] += t[u][s];
+    }
+#pragma unroll
+    for (int u = 0; u < IPT; ++u) {
+        const int idx = threadIdx.x + 256 * u, m = idx / SK_CB, gc = c0 + idx % SK_CB;
+        if (m < M && gc < N) {
+            f16* dst = Cp + (int64_t)m * N + gc;
+            *dst = (f16)(p.acc ? v[u] + (float)*dst : v[u]);
+        }
+    }
+}
+
 template <int MR>
 __global__ __launch_bounds__(256) void gemv_sk(GemmArgs p, float* __restrict__ part, unsigned* cnt) {
     // A's slice in LDS as fp16 pairs: pair P = rg + 32 v (v < SK_LD / 2) holds
@@ -746,7 +786,7 @@ __global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ p
             }
         }
     }
-    if (nks > 1) gemv_finish(p, part, cnt, c0);
+    if (nks > 1) gemv_finish_m16(p, part, cnt, c0);
 }
 
 
