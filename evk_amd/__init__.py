@@ -66,6 +66,7 @@ SIGNATURES = {
     "evkhip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
     "evkhip_flash_has_mfma": (C.c_int, [C.c_uint32]),
     "evkhip_flash_kernel_path": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32]),
+    "evkhip_kv_decode_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "evkhip_matmul": (C.c_int, [TP, TP, TP, C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_uint32,
                                 C.c_void_p]),
     "evkhip_matmul_noalloc": (C.c_int, [TP, TP, TP, C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_uint32,

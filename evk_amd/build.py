@@ -22,7 +22,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("EVK_OFFLOAD_ARCH", "gfx950")
 
 KERNEL_SOURCES = ["capi.hip", "gemm.hip", "flash.hip", "flash_wide.hip", "decode_ops.hip", "model.hip", "decode_persist.hip",
-                  "train_ops.hip"]
+                  "kv_step.hip", "train_ops.hip"]
 API_SOURCES = ["evk_runtime.cpp", "evk_ai.cpp"]
 
 HIP_FLAGS = [

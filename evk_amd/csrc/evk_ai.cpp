@@ -111,6 +111,41 @@ void single_query_attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor&
           "single_query_attention");
 }
 
+bool kv_decode_step(Tensor& token_emb, Tensor& w_out, const std::vector<DecoderLayer>& layers,
+                    const std::vector<std::unique_ptr<Tensor>>& k_cache,
+                    const std::vector<std::unique_ptr<Tensor>>& v_cache, Tensor& ids, uint32_t pos, Tensor& logits,
+                    float rope_base, float eps) {
+    if (layers.empty() || layers.size() > EVKHIP_KV_MAX_LAYERS || k_cache.size() != layers.size() ||
+        v_cache.size() != layers.size() || token_emb.shape.rank() != 2 || w_out.shape.rank() != 2 ||
+        k_cache[0]->shape.rank() != 3)
+        return false;
+    evkhip_kv_model m{};
+    m.batch = k_cache[0]->shape[0];
+    m.max_seq = k_cache[0]->shape[1];
+    m.d = token_emb.shape[1];
+    m.vocab = w_out.shape[1];
+    m.hidden = layers[0].w1->shape[1];
+    m.layers = uint32_t(layers.size());
+    m.eps = eps;
+    m.rope_base = rope_base;
+    if (ids.shape.count() != m.batch || logits.shape.count() != m.batch * m.vocab || w_out.shape[0] != m.d)
+        return false;
+    m.emb = token_emb.device_ptr();
+    m.w_out = w_out.device_ptr();
+    for (size_t l = 0; l < layers.size(); ++l) {
+        const DecoderLayer& w = layers[l];
+        Tensor* t[6] = {w.w_q, w.w_k, w.w_v, w.w_o, w.w1, w.w2};
+        for (int i = 0; i < 6; ++i) m.w[l][i] = t[i]->device_ptr();
+        m.k_cache[l] = k_cache[l]->device_ptr();
+        m.v_cache[l] = v_cache[l]->device_ptr();
+    }
+    const int rc = evkhip_kv_decode_step(&m, static_cast<const uint16_t*>(ids.device_ptr()), pos,
+                                         logits.device_ptr(), stream());
+    if (rc == EVKHIP_ERR_UNSUPPORTED) return false;
+    check(rc, "kv_decode_step");
+    return true;
+}
+
 void kv_cache_write(Tensor& src, Tensor& cache, uint32_t pos0) {
     evkhip_tensor S = desc(src), C = desc(cache);
     check(evkhip_kv_cache_write(&S, &C, pos0, stream()), "kv_cache_write");

@@ -769,6 +769,16 @@ struct DecoderLayer {
     Tensor* w2;   // (hidden, D)
 };
 
+// The fused decode step of KVCacheDecoder (no reference counterpart): one
+// launch runs one position of every sequence through all layers and writes
+// the logits (B, 1, V), with the op-by-op step's fp16 rounding points.
+// Returns false, having done nothing, when the shapes need the op-by-op
+// step (evkhip_kv_decode_step lists its limits).
+bool kv_decode_step(Tensor& token_emb, Tensor& w_out, const std::vector<DecoderLayer>& layers,
+                    const std::vector<std::unique_ptr<Tensor>>& k_cache,
+                    const std::vector<std::unique_ptr<Tensor>>& v_cache, Tensor& ids, uint32_t pos, Tensor& logits,
+                    float rope_base, float eps);
+
 // KV-cached decoding of the model example/main_llm.cpp builds with Graph
 // ops (MeshTokenModel, :549-620): embed, then per layer
 // CausalAttentionBlock::forward (:528-546) -- rms_norm, the q/k/v
@@ -815,6 +825,9 @@ public:
     }
 
     uint32_t cached() const { return len_; }
+    // step() runs the fused one-launch step (kv_decode_step) where the
+    // shapes allow it; false keeps the op-by-op step (for comparisons)
+    void set_fused(bool on) { fused_ = on; }
     Tensor& logits() { return *logits_; }
     Tensor& k_cache(uint32_t layer) { return *k_cache_[layer]; }
     Tensor& v_cache(uint32_t layer) { return *v_cache_[layer]; }
@@ -853,6 +866,10 @@ public:
         assert(ids.shape.count() == B_ && "step: one id per sequence");
         assert(len_ < S_ && "step: the caches are full");
         const uint32_t pos = len_;
+        if (fused_ && kv_decode_step(emb_, w_out_, layers_, k_cache_, v_cache_, ids, pos, *logits_, base_, eps_)) {
+            len_ = pos + 1;
+            return *logits_;
+        }
         Tensor krow = Tensor::alias(Shape({B_, 1, D_}), skr_->buffer);
         Tensor vrow = Tensor::alias(Shape({B_, 1, D_}), sv_->buffer);
         embed(emb_, ids, *sx_);
@@ -895,6 +912,7 @@ private:
     uint32_t B_, S_, D_ = 0, V_ = 0, H_ = 0;
     float base_, eps_;
     uint32_t len_ = 0;
+    bool fused_ = true;
     std::vector<std::unique_ptr<Tensor>> k_cache_, v_cache_;
     std::unique_ptr<Tensor> px_, ph_, pq_, pk_, pv_, pqr_, pkr_, po_, pt_, px1_, pu_, pg_;
     std::unique_ptr<Tensor> sx_, sh_, sq_, sk_, sv_, sqr_, skr_, so_, st_, su_, sg_;

@@ -343,6 +343,35 @@ int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* 
  * gives up raises EVKHIP_STATUS_WAIT_TIMEOUT (evkhip_device_status) and the
  * outputs of that call are then unreliable.  Calls that overlap on one GPU
  * race on the library's hand-over buffers. */
+/* Fused KV-cached decode step of evk::ai::KVCacheDecoder (no reference
+ * counterpart; the reference recomputes every position per sampled token,
+ * example/main_llm.cpp:622-654, with the blocks of main_llm.cpp:528-546):
+ * one launch runs, for each of `batch` sequences, one new position `pos`
+ * through every layer (rms_norm; q, k, v = x.Wq, x.Wk, x.Wv; rope on q and k
+ * with head size d at pos; the position's k, v written to row pos of the
+ * caches; single-head causal attention over rows [0, pos]; x += attn.Wo;
+ * x += gelu(rms_norm(x).W1).W2) and writes the logits rms_norm(x).Wout,
+ * fp16 (batch, vocab).  Every op output is rounded to fp16 as the op-by-op
+ * step rounds it.  Weights as the Graph stores them, (in, out) row-major:
+ * w[l] = {Wq, Wk, Wv, Wo (d,d), W1 (d,hidden), W2 (hidden,d)}; emb (vocab,d),
+ * w_out (d,vocab); k_cache[l], v_cache[l] (batch, max_seq, d); ids (batch)
+ * raw uint16 token ids of position pos.  Needs d, hidden, vocab multiples of
+ * 8 (d <= 2048, hidden <= 8192), max_seq <= 8192, at most
+ * EVKHIP_KV_MAX_LAYERS layers and 16-byte aligned pointers, else
+ * EVKHIP_ERR_UNSUPPORTED (the op-by-op step serves those shapes). */
+#define EVKHIP_KV_MAX_LAYERS 24
+typedef struct evkhip_kv_model {
+    uint32_t batch, d, hidden, vocab, layers, max_seq;
+    float eps, rope_base;
+    const void* emb;
+    const void* w_out;
+    const void* w[EVKHIP_KV_MAX_LAYERS][6];
+    void* k_cache[EVKHIP_KV_MAX_LAYERS];
+    void* v_cache[EVKHIP_KV_MAX_LAYERS];
+} evkhip_kv_model;
+int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_t pos, void* logits,
+                          void* stream);
+
 uint64_t evkhip_model_packed_elems(const evkhip_model_cfg* cfg);
 int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* packed, void* stream);
 int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, void* cache,

@@ -889,6 +889,8 @@ static void test_kv_decoder_matches_full_recompute() {
         t.cpu_upload();
     };
     evk::ai::KVCacheDecoder dec(emb, w_out, layers, B, S);
+    evk::ai::KVCacheDecoder dec_ops(emb, w_out, layers, B, S);  // the op-by-op step
+    dec_ops.set_fused(false);
     Tensor prompt({B, PREFIX - 1});
     {
         std::vector<uint16_t> p(B * (PREFIX - 1));
@@ -897,9 +899,10 @@ static void test_kv_decoder_matches_full_recompute() {
         put_ids(prompt, p.data());
     }
     dec.prefill(prompt);
+    dec_ops.prefill(prompt);
     Tensor ids({B}), kv_next({B}), ref_next({B});
     int mismatches = 0, ties = 0;
-    float max_dlogit = 0.0f;
+    float max_dlogit = 0.0f, max_dfused = 0.0f;
     for (uint32_t pos = PREFIX - 1; pos < PREFIX - 1 + STEPS; ++pos) {
         // reference: full recompute over every position, sample at pos
         put_ids(in, toks.data());
@@ -912,6 +915,11 @@ static void test_kv_decoder_matches_full_recompute() {
         Tensor& lg = dec.step(ids);
         evk::ai::greedy_sample(lg, kv_next, 0, BASE, BINS);
         std::vector<float> ref_l = download(logits), kv_l = download(lg);
+        {
+            // the fused one-launch step against the op-by-op step
+            std::vector<float> op_l = download(dec_ops.step(ids));
+            for (size_t i = 0; i < op_l.size(); ++i) max_dfused = std::fmax(max_dfused, std::fabs(op_l[i] - kv_l[i]));
+        }
         ref_next.cpu_download();
         kv_next.cpu_download();
         for (uint32_t b = 0; b < B; ++b) {
@@ -925,9 +933,12 @@ static void test_kv_decoder_matches_full_recompute() {
             toks[b * S + pos + 1] = r;  // teacher forcing with the recompute's id
         }
     }
-    std::printf("  %u steps x %u sequences: %d mismatches, %d near-ties, max |dlogit| %.4g\n", STEPS, B,
-                mismatches, ties, max_dlogit);
+    std::printf("  %u steps x %u sequences: %d mismatches, %d near-ties, max |dlogit| %.4g (fused vs op-by-op "
+                "step %.4g)\n",
+                STEPS, B, mismatches, ties, max_dlogit, max_dfused);
     TEST(dec.cached() == PREFIX - 1 + STEPS);
+    TEST(dec_ops.cached() == PREFIX - 1 + STEPS);
+    TEST(max_dfused < 1e-2f);
     TEST(mismatches == 0);
     TEST(max_dlogit < 1e-2f);
 }

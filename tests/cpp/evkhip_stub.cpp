@@ -106,6 +106,13 @@ int evkhip_single_query_attention(const evkhip_tensor* q, const evkhip_tensor* k
                                   const evkhip_tensor* out, uint32_t L, uint32_t heads, void* stream) {
     return record("single_query_attention", {q, kc, vc, out}, {L, heads}, {}, stream);
 }
+int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_t pos, void* logits, void* stream) {
+    // the host mock has no kernels: report the shape as unsupported, so the
+    // decoder takes its op-by-op step (which the stub records)
+    (void)record("kv_decode_step", {}, {m ? (long long)m->layers : 0, pos}, {}, stream, ids);
+    (void)logits;
+    return EVKHIP_ERR_UNSUPPORTED;
+}
 int evkhip_kv_cache_write(const evkhip_tensor* src, const evkhip_tensor* cache, uint32_t pos0, void* stream) {
     return record("kv_cache_write", {src, cache}, {pos0}, {}, stream);
 }

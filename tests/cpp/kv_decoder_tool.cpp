@@ -28,6 +28,8 @@
 //                         ids downloaded every step as the reference's loop does
 //         kv_device_ids   the same, each step fed the previous step's ids on
 //                         the device; one synchronisation at the end
+//         kv_op_by_op     kv_device_ids with the op-by-op step (16 launches a
+//                         layer) instead of the fused one-launch step
 //       Both paths compute the same logits up to rounding (the oracle test
 //       checks the decoder); a near-tie can send a sequence down another
 //       path, which changes none of the timed work.
@@ -228,7 +230,8 @@ double run_full(Model& m, std::vector<uint16_t>& toks) {
 
 // KVCacheDecoder over the same positions; host_ids: download the ids every
 // step (the reference loop's pattern), else feed them on the device.
-double run_kv(Model& m, evk::ai::KVCacheDecoder& dec, std::vector<uint16_t>& toks, bool host_ids) {
+double run_kv(Model& m, evk::ai::KVCacheDecoder& dec, std::vector<uint16_t>& toks, bool host_ids, bool fused = true) {
+    dec.set_fused(fused);
     Tensor pre({B, PROMPT}), ids_a({B}), ids_b({B});
     std::vector<uint16_t> p(B * PROMPT), first(B);
     for (uint32_t b = 0; b < B; ++b) {
@@ -273,16 +276,20 @@ int bench(int reps) {
     const double full = best([&](std::vector<uint16_t>& t) { return run_full(m, t); });
     const double kvh = best([&](std::vector<uint16_t>& t) { return run_kv(m, dec, t, true); });
     const double kvd = best([&](std::vector<uint16_t>& t) { return run_kv(m, dec, t, false); });
+    const double kvo = best([&](std::vector<uint16_t>& t) { return run_kv(m, dec, t, false, false); });
     const double n_tok = double(B) * (LAST - FIRST);
     std::printf("{\"workload\": \"example/main_llm.cpp sample_autoregressive: B=%u, D=%u (1 head), hidden %u, "
                 "%u layers, vocab %u, positions %u..%u\", \"ids_per_sequence\": %u, "
                 "\"full_recompute_ms\": %.3f, \"full_recompute_tokens_per_s\": %.1f, "
                 "\"kv_host_ids_ms\": %.3f, \"kv_host_ids_tokens_per_s\": %.1f, "
                 "\"kv_device_ids_ms\": %.3f, \"kv_device_ids_tokens_per_s\": %.1f, "
-                "\"speedup_kv_host_ids\": %.2f, \"speedup_kv_device_ids\": %.2f, \"timing\": \"best of %d runs "
-                "after one warm-up, host wall clock around the whole loop\"}\n",
+                "\"kv_op_by_op_ms\": %.3f, \"kv_op_by_op_tokens_per_s\": %.1f, "
+                "\"speedup_kv_host_ids\": %.2f, \"speedup_kv_device_ids\": %.2f, \"step\": \"fused: one launch "
+                "per position (evkhip_kv_decode_step); op_by_op: 16 launches a layer\", \"timing\": \"best of %d "
+                "runs after one warm-up, host wall clock around the whole loop\"}\n",
                 B, D, HID, L, V, FIRST, LAST - 1, LAST - FIRST, full, n_tok / (full * 1e-3), kvh,
-                n_tok / (kvh * 1e-3), kvd, n_tok / (kvd * 1e-3), full / kvh, full / kvd, reps);
+                n_tok / (kvh * 1e-3), kvd, n_tok / (kvd * 1e-3), kvo, n_tok / (kvo * 1e-3), full / kvh, full / kvd,
+                reps);
     return 0;
 }
 
