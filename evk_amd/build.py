@@ -89,6 +89,25 @@ def build(verbose: bool = False) -> None:
         print("built", kern)
 
 
+def build_decode_trace(verbose: bool = False) -> str:
+    """evk_amd/_trace/libevkhip.so: the library with the persistent decode's
+    stage timestamps compiled in (EVKHIP_DECODE_TRACE); evk_amd/decode_trace.py
+    loads it.  The other objects come from the last build()."""
+    out_dir = os.path.join(HERE, "_trace")
+    os.makedirs(out_dir, exist_ok=True)
+    obj = os.path.join(out_dir, "decode_persist.hip.o")
+    _run([HIPCC] + HIP_FLAGS + ["-DEVKHIP_DECODE_TRACE", "-c", os.path.join(CSRC, "decode_persist.hip"), "-o", obj])
+    objs = [obj if s == "decode_persist.hip" else os.path.join(BUILD, s + ".o") for s in KERNEL_SOURCES]
+    lib = os.path.join(out_dir, "libevkhip.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib + ".tmp"] + objs)
+    os.replace(lib + ".tmp", lib)
+    if verbose:
+        print("built", lib)
+    return lib
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    if "--decode-trace" in sys.argv:
+        build_decode_trace(verbose=True)
     sys.exit(0)

@@ -62,6 +62,24 @@ constexpr int YO = 144;            // stage output floats (>= head rows per slot
 
 __device__ unsigned g_dec_status;
 
+#ifdef EVKHIP_DECODE_TRACE
+// Stage timestamps of one step and layer (a separate trace build of the
+// library, evk_amd/build.py --decode-trace): per workgroup and stage kind
+// S1..S5, the 100 MHz wall clock when the stage starts, when its input has
+// arrived and when its outputs are stored.
+constexpr int kTraceStep = 3, kTraceLayer = 2;
+__device__ unsigned long long g_dec_trace[1024][5][3];
+#define DEC_TRACE(c, i)                                                                                 \
+    do {                                                                                                \
+        if (threadIdx.x == 0 && (c).t == kTraceStep && (c).l == kTraceLayer && (c).k < K_HEAD)          \
+            g_dec_trace[blockIdx.x][(c).k][(i)] = __builtin_amdgcn_s_memrealtime();                     \
+    } while (0)
+#else
+#define DEC_TRACE(c, i) \
+    do {                \
+    } while (0)
+#endif
+
 struct PArgs {
     int d, H, dh, hid, V, L;
     int max_seq;
@@ -636,6 +654,7 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
         if (streamer) n2 = stream(c2, ring + (size_t)((si + 2) % NBUF) * (a.bufb / 2));
         const int t = cur.t, l = cur.l, p = l & 1, k0 = l * 5, pos = a.pos0 + t;
         const int S = splits(t);
+        DEC_TRACE(cur, 0);
         // ---- the stage's input ----
         if (!streamer) {
             // the stage's input words (one poll call site keeps the kernel's code small)
@@ -684,6 +703,7 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             fail();
             return;
         }
+        DEC_TRACE(cur, 1);
         const int tid = tid_now(), lane = tid & 63, wave = tid >> 6;
 
         // ---- the stage ----
@@ -1004,6 +1024,7 @@ __global__ __launch_bounds__(PNT) void decode_persist(PArgs a) {
             }
         }
         __syncthreads();  // the slot, mbuf and yo are reused by the next stages
+        DEC_TRACE(cur, 2);
         cur = c1;
         c1 = c2;
         c2 = next(c2);
@@ -1172,6 +1193,16 @@ int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* pa
     EVK_HIP(transpose(src + wo, dst + wo, d, V, st));  // Wout (d, V)
     return EVKHIP_OK;
 }
+
+#ifdef EVKHIP_DECODE_TRACE
+// The trace of the last launch (trace build only): 1024 x 5 x 3 uint64.
+int evkhip_debug_decode_trace(void* dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_dec_trace), sizeof(g_dec_trace), 0, hipMemcpyDeviceToHost) ==
+                   hipSuccess
+               ? EVKHIP_OK
+               : EVKHIP_ERR_HIP;
+}
+#endif
 
 int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, void* cache, uint16_t* token_io,
                                uint32_t n_steps, uint32_t pos0, void* logits, void* stream) {
