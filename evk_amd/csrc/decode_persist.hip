@@ -1194,6 +1194,17 @@ int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* pa
     return EVKHIP_OK;
 }
 
+int evkhip_debug_decode_set_epoch(uint32_t distance) {
+    EVK_RETURN_IF(!g_pws.buf, EVKHIP_ERR_INVALID_ARG,
+                  "debug_decode_set_epoch: no persistent decode has run on this device yet");
+    EVK_RETURN_IF(distance >= kWrapAt, EVKHIP_ERR_INVALID_ARG, "debug_decode_set_epoch: distance %u too large",
+                  distance);
+    const uint32_t base = kWrapAt - distance;
+    EVK_HIP(hipDeviceSynchronize());
+    EVK_HIP(hipMemcpy(g_pws.buf, &base, sizeof(base), hipMemcpyHostToDevice));
+    return EVKHIP_OK;
+}
+
 #ifdef EVKHIP_DECODE_TRACE
 // The trace of the last launch (trace build only): 1024 x 5 x 3 uint64.
 int evkhip_debug_decode_trace(void* dst) {

@@ -372,6 +372,12 @@ typedef struct evkhip_kv_model {
 int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_t pos, void* logits,
                           void* stream);
 
+/* Test hook of evkhip_model_decode_packed (no reference counterpart): sets
+ * the hand-over epoch of this device's persistent decode `distance` tags
+ * below the point where the tags wrap, so that the next launch that needs
+ * more tags than that clears the mailboxes and restarts them from zero.
+ * Synchronises the device; needs a persistent decode to have run on it. */
+int evkhip_debug_decode_set_epoch(uint32_t distance);
 uint64_t evkhip_model_packed_elems(const evkhip_model_cfg* cfg);
 int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* packed, void* stream);
 int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, void* cache,

@@ -326,6 +326,46 @@ def test_decode_packed_repeated_and_replayed(dev, orc):
     assert evk.device_status(clear=True) == 0
 
 
+def test_decode_packed_tag_wrap(dev, orc):
+    """The hand-over tags wrap: launches near the end of the tag range clear
+    the mailboxes and restart the tags from zero behind a barrier of every
+    workgroup.  Set just below the wrap point, a launch that still fits, one
+    that wraps, and the ones after it give the same ids and logits as a
+    launch far from it, and none reports a wait timeout."""
+    import evk_amd as evk
+    import torch
+    kw = dict(vocab=512, d=128, heads=2, layers=2, hidden=256, max_seq=64)
+    ocfg, cfg = orc.model_cfg(**kw), evk.model_cfg(**kw)
+    w = orc.model_weights(ocfg, seed=371, std=0.1)
+    prompt = orc.tokens_u16(40, 372, 512)
+    W = to_dev(w, dev)
+    cache = torch.zeros(evk.model_cache_elems(cfg), dtype=torch.float16, device=dev)
+    tok = torch.zeros(9, dtype=torch.int16, device=dev)
+    logits = torch.empty(cfg.vocab, dtype=torch.float16, device=dev)
+    evk.model_prefill(cfg, W, cache, torch.from_numpy(prompt.view(np.int16)).to(dev), 0, tok, logits)
+    P = torch.empty(evk.model_packed_elems(cfg), dtype=torch.float16, device=dev)
+    evk.model_pack(cfg, W, P)
+    torch.cuda.synchronize()
+    first = tok[0].clone()
+
+    def run():
+        tok[0] = first
+        evk.model_decode_packed(cfg, P, cache, tok, 8, 40, logits)
+        torch.cuda.synchronize()
+        return tok.clone(), logits.clone()
+
+    evk.device_status(clear=True)
+    want_tok, want_lg = run()
+    # a launch takes 8 steps x (5 stages x 2 layers + the head) + 2 = 90 tags
+    need = 8 * (5 * 2 + 1) + 2
+    for distance in (need + 1, 1):  # first a launch that fits, then one that wraps at once
+        evk.debug_decode_set_epoch(distance)
+        for _ in range(3):
+            t, lg = run()
+            assert torch.equal(t, want_tok) and torch.equal(lg, want_lg), f"distance {distance}"
+    assert evk.device_status(clear=True) == 0
+
+
 def test_decode_packed_wait_timeout_is_reported(dev, orc):
     """A spin limit of one round (set from the host) makes the persistent
     decode's hand-over waits give up: every workgroup leaves, the call's
