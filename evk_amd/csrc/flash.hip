@@ -444,8 +444,11 @@ __global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
 //       and comes back transposed by ds_read_b64_tr_b16; P^T is already in
 //       B-operand order (slot s <-> key 4g+s for s < 4, 16+4g+s-4 after).
 //   row sums: ones . P^T on the MFMA.
-// The next chunk's K and V are prefetched into registers during the current
-// chunk.  Rescaling is lazy (RESCALE_LOG2), as in flash_fwd.
+// The next chunk's V is requested once the current one is in its LDS slot,
+// its K once the score MFMAs have read the current K registers (no register
+// copies); past a wave's last chunk the requests get an empty descriptor, so
+// the loop has no branch around them.  Rescaling is lazy (RESCALE_LOG2), as
+// in flash_fwd.
 // ---------------------------------------------------------------------------
 constexpr int KC = 32;  // keys per chunk
 #ifndef FWD_KS_QB
@@ -516,16 +519,27 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     const uint32_t k_vo = (uint32_t)(l16 * DH + g * 8) * 2;
     const uint32_t v_vo = (uint32_t)lane * 16;
     u32x4 kr[2][KS], vr[VPER];
-    auto load_chunk = [&](int c) {
-        const uint32_t rem = (uint32_t)(N - c * KC) * DH * 2;
-        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (int64_t)c * KC * DH, rem);
-        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (int64_t)c * KC * DH, rem);
+    // a chunk past the wave's last gets an empty descriptor: its loads
+    // return zeros without touching memory, and the loop needs no branch
+    auto load_k = [&](int c) {
+        const bool ok = c < nch;
+        const uint32_t rem = ok ? (uint32_t)(N - c * KC) * DH * 2 : 0u;
+        const __amdgpu_buffer_rsrc_t kres = buf_rsrc(kb_ptr + (ok ? (int64_t)c * KC * DH : 0), rem);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) kr[kb][ks] = buf_load16(kres, k_vo + kb * 16 * DH * 2 + ks * 64, 0);
+    };
+    auto load_v = [&](int c) {
+        const bool ok = c < nch;
+        const uint32_t rem = ok ? (uint32_t)(N - c * KC) * DH * 2 : 0u;
+        const __amdgpu_buffer_rsrc_t vres = buf_rsrc(vb_ptr + (ok ? (int64_t)c * KC * DH : 0), rem);
 #pragma unroll
         for (int i = 0; i < VPER; ++i) vr[i] = buf_load16(vres, v_vo + i * 1024, 0);
+    };
+    auto load_chunk = [&](int c) {
+        load_k(c);
+        load_v(c);
     };
 
     // The heavy tile's first chunk goes out before the Q staging (K and V do
@@ -567,13 +581,15 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 
     floatx4 oacc[DB][QB];
     floatx4 lacc[QB];
-    float m_ref[QB];
+    float m_ref[QB], nbase[QB];  // nbase: -m_ref, or 0 while a row has no reference
+    bool fresh = true;           // some row of the wave may have no reference yet (wave-uniform)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int d = 0; d < DB; ++d) oacc[d][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc[qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         m_ref[qb] = -INFINITY;
+        nbase[qb] = 0.0f;
     }
     const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f,
                          (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
@@ -586,11 +602,6 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     auto chunk = [&](int c, auto mtag) {
         constexpr bool MASK = decltype(mtag)::value;
         const int key0 = c * KC;
-        half8 kf[2][KS];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kf[kb][ks] = as_half8(kr[kb][ks]);
         // V chunk into this wave's slot (LDS ops of a wave complete in order,
         // so the previous chunk's transposed reads are done)
 #pragma unroll
@@ -598,7 +609,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             const int idx = lane + 64 * i;
             *reinterpret_cast<u32x4*>(vslot + (idx / (DH / 8)) * VW + (idx % (DH / 8)) * 8) = vr[i];
         }
-        if (c + 4 < nch) load_chunk(c + 4);
+        load_v(c + 4);
         // V^T fragments read back at once (after the slot's writes, in
         // order): their latency hides behind the score MFMAs
         half8 vt[DB];
@@ -615,7 +626,10 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb)
-                    s[kb][qb] = mfma16(kf[kb][ks], qf[qb][ks], ks == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : s[kb][qb]);
+                    s[kb][qb] = mfma16(as_half8(kr[kb][ks]), qf[qb][ks], ks == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : s[kb][qb]);
+        // the K registers are free once the score MFMAs have read them: the
+        // next chunk's K goes straight into them (no copy)
+        load_k(c + 4);
         // element j of s[kb][qb]: key key0 + 16 kb + 4 g + j, query row R0 + 16 qb + l16
         if constexpr (MASK) {
 #pragma unroll
@@ -637,20 +651,17 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         auto make_p = [&]() {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                const float nbase = (m_ref[qb] == -INFINITY) ? 0.0f : -m_ref[qb];
                 float e[2][4];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) e[kb][j] = fast_exp2(__builtin_fmaf(s[kb][qb][j], c2, nbase));
+                    for (int j = 0; j < 4; ++j) e[kb][j] = fast_exp2(__builtin_fmaf(s[kb][qb][j], c2, nbase[qb]));
                 u32x4 u = {pack_h2(e[0][0], e[0][1]), pack_h2(e[0][2], e[0][3]),
                            pack_h2(e[1][0], e[1][1]), pack_h2(e[1][2], e[1][3])};
                 pb[qb] = as_half8(u);
             }
         };
-        bool need = false;
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) need |= m_ref[qb] == -INFINITY;
+        bool need = fresh;
         make_p();
         {
             half2_t hv[4 * QB];
@@ -682,7 +693,13 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                 for (int d = 0; d < DB; ++d) oacc[d][qb] *= alpha;
                 lacc[qb] *= alpha;
                 m_ref[qb] = m_new;
+                nbase[qb] = (m_new == -INFINITY) ? 0.0f : -m_new;
             }
+            // rows whose keys so far were all masked still have no reference
+            bool none = false;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) none |= m_ref[qb] == -INFINITY;
+            fresh = __any(none);
             make_p();
         }
 #pragma unroll
@@ -693,7 +710,8 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             for (int qb = 0; qb < QB; ++qb) oacc[d][qb] = mfma16(vt[d], pb[qb], oacc[d][qb]);
         }
     };
-    for (; c < min(nch, cu); c += 4) chunk(c, std::false_type{});
+    const int c_mask = __builtin_amdgcn_readfirstlane(min(nch, cu));
+    for (; c < c_mask; c += 4) chunk(c, std::false_type{});
     for (; c < nch; c += 4) chunk(c, std::true_type{});
 
     // ---- merge the four waves' partial softmax states ----
