@@ -550,7 +550,11 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     // us, 13.0 -> 12.5 us per C2 launch).
     int c = wave;
     const bool late = CAUSAL && half == 1;
-    if (!late && c < nch) load_chunk(c);
+    // Every wave issues these requests (the late ones get the empty
+    // descriptor): with no branch around them the staging's wait counts
+    // stay exact, and the Q staging waits for the Q loads alone, not for the
+    // first chunk's K and V behind them.
+    load_k(late ? nch : c);
 
     // Q^T B operands: query R0 + 16 qb + l16, dh [32 ks + 8 g, +8)
     // the tile's Q goes through LDS once (each wave of the half loads a
@@ -562,10 +566,17 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         constexpr int QPER = QPIECES / 256;
         f16* qs = vslot_all;                              // [ROWS][DH + 8]
         const int ht = threadIdx.x & 255;
+        u32x4 qv[QPER];
 #pragma unroll
         for (int u = 0; u < QPER; ++u) {
             const int pc = ht + 256 * u, r = pc / (DH / 8), cc = (pc % (DH / 8)) * 8;
-            *reinterpret_cast<u32x4*>(qs + r * (DH + 8) + cc) = buf_load16(qres, (uint32_t)(r * DH + cc) * 2, 0);
+            qv[u] = buf_load16(qres, (uint32_t)(r * DH + cc) * 2, 0);
+        }
+        load_v(late ? nch : c);
+#pragma unroll
+        for (int u = 0; u < QPER; ++u) {
+            const int pc = ht + 256 * u, r = pc / (DH / 8), cc = (pc % (DH / 8)) * 8;
+            *reinterpret_cast<u32x4*>(qs + r * (DH + 8) + cc) = qv[u];
         }
         __syncthreads();
 #pragma unroll
@@ -577,7 +588,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         }
         __syncthreads();  // the V slots reuse this space
     }
-    if (late && c < nch) load_chunk(c);
+    if (late) load_chunk(c);
 
     floatx4 oacc[DB][QB];
     floatx4 lacc[QB];
