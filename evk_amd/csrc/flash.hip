@@ -464,8 +464,13 @@ struct KsLayout {
     static constexpr int VSLOT = KC * VW;        // halves per wave slot
     static constexpr int VPER = KC * DH / 8 / 64;  // 16-byte V pieces per lane
     static constexpr int OW = DH + 4;            // merge row stride (floats)
-    static constexpr int MERGE = 4 * ROWS * OW + 2 * 4 * ROWS;  // O partials, m, l of the four waves
-    static constexpr int LDS_BYTES = (MERGE * 4 > 4 * VSLOT * 2) ? MERGE * 4 : 4 * VSLOT * 2;
+    // the merge area follows the V slots: a wave stores its partials as soon
+    // as its own loop ends, while other waves still use their slots.  Each
+    // wave stores the three 16-row blocks it does not finish, and m, l of all
+    // its rows.
+    static constexpr int VBYTES = 4 * VSLOT * 2;
+    static constexpr int MERGE = 4 * (QB - 1) * 16 * OW + 2 * 4 * ROWS;  // floats
+    static constexpr int LDS_BYTES = VBYTES + MERGE * 4;
 };
 
 template <int DH, int QB, bool CAUSAL>
@@ -754,12 +759,13 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                                   __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
-    half_sync(4);  // every wave of the half is done with its V slot
-    float* ob = smem_f;                          // [wave][ROWS][OW]
-    float* mw = smem_f + 4 * ROWS * L::OW;       // [wave][ROWS]
+    static_assert(QB == 4, "one 16-row block per wave of the half");
+    float* ob = smem_f + L::VBYTES / 4;          // [wave][3 blocks][16][OW]
+    float* mw = ob + 4 * (QB - 1) * 16 * L::OW;  // [wave][ROWS]
     float* lw = mw + 4 * ROWS;                   // [wave][ROWS]
     // wave w finishes the rows of its block qb = w; it stores the other
-    // blocks' partial state for the waves that finish them and keeps its own
+    // blocks' partial state for the waves that finish them (block qb in its
+    // slot qb, or qb - 1 past its own) and keeps its own
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int q = qb * 16 + ml16;
@@ -768,13 +774,14 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             lw[wave * ROWS + q] = lacc[qb][0];
         }
         if (qb != wave) {
+            const int k = qb < wave ? qb : qb - 1;
 #pragma unroll
             for (int d = 0; d < DB; ++d)
-                *reinterpret_cast<floatx4*>(ob + (wave * ROWS + q) * L::OW + d * 16 + mg * 4) = oacc[d][qb];
+                *reinterpret_cast<floatx4*>(ob + ((wave * (QB - 1) + k) * 16 + ml16) * L::OW + d * 16 + mg * 4) =
+                    oacc[d][qb];
         }
     }
-    half_sync(8);
-    static_assert(QB == 4, "one 16-row block per wave of the half");
+    half_sync(4);
     // lane (mg, ml16): row q = 16 wave + ml16, dh 16 d + 4 mg + j
     const int q = wave * 16 + ml16;
     float mv[4], m = -INFINITY;
@@ -807,9 +814,10 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 #pragma unroll
             for (int d = 0; d < DB; ++d) a[d] += sc * r[d];
         } else {
+            const int k = wave < w ? wave : wave - 1;  // this block's slot in wave w
 #pragma unroll
             for (int d = 0; d < DB; ++d)
-                a[d] += sc * *reinterpret_cast<const floatx4*>(ob + (w * ROWS + q) * L::OW + d * 16 + mg * 4);
+                a[d] += sc * *reinterpret_cast<const floatx4*>(ob + ((w * (QB - 1) + k) * 16 + ml16) * L::OW + d * 16 + mg * 4);
         }
     }
     const int row = R0 + q;
