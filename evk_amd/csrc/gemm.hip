@@ -547,43 +547,42 @@ DEV void gemv_finish(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
     }
 }
 
-// The same finish for up to 16 rows (the MFMA kernel): a thread's items
-// (m, column) are idx = tid + 256 u; every partial of all of them is
-// requested before any is added (one round trip to the coherence point
-// instead of one per item), then each item's partials are added in range
-// order, as in gemv_finish.
+// The same finish for up to 16 rows (the MFMA kernel), with 16-byte loads:
+// thread t adds row t / 16, columns 4 (t % 16) .. +3 of the column block,
+// every range's partial requested before any is added, in range order as
+// in gemv_finish.  The loads carry the sc1 policy of ld_ag (served from the
+// device coherence point).
 DEV void gemv_finish_m16(const GemmArgs& p, float* part, unsigned* cnt, int c0) {
     const int M = p.M, N = p.N, bz = blockIdx.z, nks = gridDim.y;
     if (!arrive_last(cnt + bz * gridDim.x + blockIdx.x, nks)) return;
-    f16* Cp = p.C + (int64_t)bz * p.sC;
-    const int64_t stride = (int64_t)M * N;
-    constexpr int IPT = 16 * SK_CB / 256;   // items per thread at M = 16
-    constexpr int PB = 8;                    // ranges per batch of loads
-    float v[IPT];
-#pragma unroll
-    for (int u = 0; u < IPT; ++u) v[u] = 0.0f;
+    static_assert(16 * SK_CB / 4 == 256, "one row quad per thread");
+    const int m = threadIdx.x / (SK_CB / 4), gc = c0 + (threadIdx.x % (SK_CB / 4)) * 4;
+    const bool ok = m < M && gc < N;  // N % 8 == 0: the quad is whole
+    const __amdgpu_buffer_rsrc_t pres =
+        buf_rsrc(part + (int64_t)bz * nks * M * N, (uint32_t)((int64_t)nks * M * N * 4));
+    const uint32_t off0 = (uint32_t)(((int64_t)m * N + gc) * 4), step = (uint32_t)((int64_t)M * N * 4);
+    constexpr int PB = 8;  // ranges per batch of loads
+    floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < nks; s0 += PB) {
-        float t[IPT][PB];
+        u32x4 t[PB];
 #pragma unroll
-        for (int u = 0; u < IPT; ++u) {
-            const int idx = threadIdx.x + 256 * u, m = idx / SK_CB, gc = c0 + idx % SK_CB;
-            const bool ok = m < M && gc < N;
-            const float* src = part + ((int64_t)bz * nks * M + m) * N + gc;
+        for (int s = 0; s < PB; ++s)
+            t[s] = __builtin_amdgcn_raw_buffer_load_b128(pres, oob_or(ok && s0 + s < nks, off0 + (s0 + s) * step), 0,
+                                                         16 /* sc1 */);
 #pragma unroll
-            for (int s = 0; s < PB; ++s) t[u][s] = (ok && s0 + s < nks) ? ld_ag(src + (s0 + s) * stride) : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < IPT; ++u)
-#pragma unroll
-            for (int s = 0; s < PB; ++s) v[u] += t[u][s];
+        for (int s = 0; s < PB; ++s) v += __builtin_bit_cast(floatx4, t[s]);
     }
-#pragma unroll
-    for (int u = 0; u < IPT; ++u) {
-        const int idx = threadIdx.x + 256 * u, m = idx / SK_CB, gc = c0 + idx % SK_CB;
-        if (m < M && gc < N) {
-            f16* dst = Cp + (int64_t)m * N + gc;
-            *dst = (f16)(p.acc ? v[u] + (float)*dst : v[u]);
+    if (ok) {
+        f16* dst = p.C + (int64_t)bz * p.sC + (int64_t)m * N + gc;
+        if (p.acc) {
+            const uint2 o = *reinterpret_cast<const uint2*>(dst);
+            const half2_t h0 = __builtin_bit_cast(half2_t, o.x), h1 = __builtin_bit_cast(half2_t, o.y);
+            v[0] += (float)h0[0];
+            v[1] += (float)h0[1];
+            v[2] += (float)h1[0];
+            v[3] += (float)h1[1];
         }
+        *reinterpret_cast<uint2*>(dst) = uint2{pack_h2(v[0], v[1]), pack_h2(v[2], v[3])};
     }
 }
 
