@@ -773,19 +773,33 @@ __global__ __launch_bounds__(256) void gemv_mf(GemmArgs p, float* __restrict__ p
     }
     // D: column c0 + 16 wave + l16, rows 4 g + j
     const int gc = c0 + wave * 16 + l16;
+    if (nks == 1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = 4 * g + j;
-        if (m < M && gc < N) {
-            if (nks == 1) {
+        for (int j = 0; j < 4; ++j) {
+            const int m = 4 * g + j;
+            if (m < M && gc < N) {
                 f16* dst = Cp + (int64_t)m * N + gc;
                 *dst = (f16)(p.acc ? acc[j] + (float)*dst : acc[j]);
-            } else {
-                st_ag(part + (((int64_t)bz * nks + ks) * M + m) * N + gc, acc[j]);
             }
         }
+        return;
     }
-    if (nks > 1) gemv_finish_m16(p, part, cnt, c0);
+    // the partial goes out as 16-byte row pieces: through LDS (the B stage
+    // is free after the last barrier), thread t stores row t / 16, columns
+    // 4 (t % 16) .. +3, written through (sc1) like the agent-scope stores
+    float* ps = reinterpret_cast<float*>(bs);  // [16][SK_CB]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ps[(4 * g + j) * SK_CB + wave * 16 + l16] = acc[j];
+    __syncthreads();
+    {
+        const int m = threadIdx.x / (SK_CB / 4), q = (threadIdx.x % (SK_CB / 4)) * 4;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ps + m * SK_CB + q);
+        const __amdgpu_buffer_rsrc_t pres =
+            buf_rsrc(part + ((int64_t)bz * nks + ks) * M * N, (uint32_t)((int64_t)M * N * 4));
+        __builtin_amdgcn_raw_buffer_store_b128(v, pres, oob_or(m < M && c0 + q < N, (uint32_t)(((int64_t)m * N + c0 + q) * 4)),
+                                               0, 16 /* sc1 */);
+    }
+    gemv_finish_m16(p, part, cnt, c0);
 }
 
 
