@@ -446,14 +446,23 @@ __global__ __launch_bounds__(512) void flash_fwd(FlashArgs p, int round) {
 //   row sums: ones . P^T on the MFMA.
 // The next chunk's V is requested once the current one is in its LDS slot,
 // its K once the score MFMAs have read the current K registers (no register
-// copies); past a wave's last chunk the requests get an empty descriptor, so
-// the loop has no branch around them.  Rescaling is lazy (RESCALE_LOG2), as
-// in flash_fwd.
+// copies); a wave's last chunk requests nothing, so leaving the loop waits
+// for no load.  Rescaling is lazy (RESCALE_LOG2), as in flash_fwd; the
+// row maxima of a rescale cross the wave's 16-lane rows by permlane swaps.
 // ---------------------------------------------------------------------------
 constexpr int KC = 32;  // keys per chunk
 #ifndef FWD_KS_QB
 #define FWD_KS_QB 4  // 16-row query blocks per wave (rows per workgroup / 16)
 #endif
+
+// Maximum over the four 16-lane rows of a wave (lanes 16 and 32 apart):
+// two row swaps on the VALU instead of cross-lane LDS permutes.
+DEV float max_over_lane_rows(float m) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
 
 template <int DH, int QB>
 struct KsLayout {
@@ -525,7 +534,8 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     const uint32_t v_vo = (uint32_t)lane * 16;
     u32x4 kr[2][KS], vr[VPER];
     // a chunk past the wave's last gets an empty descriptor: its loads
-    // return zeros without touching memory, and the loop needs no branch
+    // return zeros without touching memory (the start-up requests of the
+    // late waves use this to stay branch-free)
     auto load_k = [&](int c) {
         const bool ok = c < nch;
         const uint32_t rem = ok ? (uint32_t)(N - c * KC) * DH * 2 : 0u;
@@ -597,14 +607,20 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
 
     floatx4 oacc[DB][QB];
     floatx4 lacc[QB];
-    float m_ref[QB], nbase[QB];  // nbase: -m_ref, or 0 while a row has no reference
+    // the running reference of a row is m_ref = -nbase once the row has one
+    // (bit qb of refbits, per lane); nbase is 0 until then
+    float nbase[QB];
+    uint32_t refbits = 0;
+    auto mref = [&](int qb) { return ((refbits >> qb) & 1) ? -nbase[qb] : -INFINITY; };
     bool fresh = true;           // some row of the wave may have no reference yet (wave-uniform)
+    // no row has had a reference yet: O and l are still zero, so the first
+    // rescale has nothing to scale (wave-uniform)
+    bool any_ref = false;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int d = 0; d < DB; ++d) oacc[d][qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc[qb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        m_ref[qb] = -INFINITY;
         nbase[qb] = 0.0f;
     }
     const half8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f,
@@ -625,7 +641,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
             const int idx = lane + 64 * i;
             *reinterpret_cast<u32x4*>(vslot + (idx / (DH / 8)) * VW + (idx % (DH / 8)) * 8) = vr[i];
         }
-        load_v(c + 4);
+        if (c + 4 < nch) load_v(c + 4);
         // V^T fragments read back at once (after the slot's writes, in
         // order): their latency hides behind the score MFMAs
         half8 vt[DB];
@@ -645,7 +661,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                     s[kb][qb] = mfma16(as_half8(kr[kb][ks]), qf[qb][ks], ks == 0 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : s[kb][qb]);
         // the K registers are free once the score MFMAs have read them: the
         // next chunk's K goes straight into them (no copy)
-        load_k(c + 4);
+        if (c + 4 < nch) load_k(c + 4);
         // element j of s[kb][qb]: key key0 + 16 kb + 4 g + j, query row R0 + 16 qb + l16
         if constexpr (MASK) {
 #pragma unroll
@@ -677,9 +693,11 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
                 pb[qb] = as_half8(u);
             }
         };
+        // while some row of the wave has no reference the rescale below runs
+        // anyway and forms the probabilities itself
         bool need = fresh;
-        make_p();
-        {
+        if (!fresh) {
+            make_p();
             half2_t hv[4 * QB];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
@@ -697,25 +715,31 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         }
         if (__builtin_expect(__any(need), 0)) {
             asm volatile("" ::: "memory");
+            float m_new[QB];
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-                float m = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
-                                fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
-                m = fmaxf(m, __shfl_xor(m, 16, 64));
-                m = fmaxf(m, __shfl_xor(m, 32, 64));
-                const float m_new = fmaxf(m_ref[qb], m);
-                const float alpha = (m_ref[qb] == -INFINITY) ? 0.0f : fast_exp2(m_ref[qb] - m_new);
+                const float m = fmaxf(fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3])),
+                                      fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * c2;
+                m_new[qb] = fmaxf(mref(qb), max_over_lane_rows(m));
+            }
+            if (any_ref) {
 #pragma unroll
-                for (int d = 0; d < DB; ++d) oacc[d][qb] *= alpha;
-                lacc[qb] *= alpha;
-                m_ref[qb] = m_new;
-                nbase[qb] = (m_new == -INFINITY) ? 0.0f : -m_new;
+                for (int qb = 0; qb < QB; ++qb) {
+                    const float alpha = ((refbits >> qb) & 1) ? fast_exp2(-nbase[qb] - m_new[qb]) : 0.0f;
+#pragma unroll
+                    for (int d = 0; d < DB; ++d) oacc[d][qb] *= alpha;
+                    lacc[qb] *= alpha;
+                }
+            }
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                const bool has = m_new[qb] != -INFINITY;
+                nbase[qb] = has ? -m_new[qb] : 0.0f;
+                refbits |= (uint32_t)has << qb;
             }
             // rows whose keys so far were all masked still have no reference
-            bool none = false;
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) none |= m_ref[qb] == -INFINITY;
-            fresh = __any(none);
+            fresh = __any(refbits != (1u << QB) - 1);
+            any_ref = true;
             make_p();
         }
 #pragma unroll
@@ -770,7 +794,7 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
     for (int qb = 0; qb < QB; ++qb) {
         const int q = qb * 16 + ml16;
         if (mg == 0) {
-            mw[wave * ROWS + q] = m_ref[qb];
+            mw[wave * ROWS + q] = mref(qb);
             lw[wave * ROWS + q] = lacc[qb][0];
         }
         if (qb != wave) {
@@ -782,43 +806,43 @@ __global__ __launch_bounds__(512, 1) void flash_fwd_ks(FlashArgs p) {
         }
     }
     half_sync(4);
-    // lane (mg, ml16): row q = 16 wave + ml16, dh 16 d + 4 mg + j
+    // lane (mg, ml16): row q = 16 wave + ml16, dh 16 d + 4 mg + j.  Every LDS
+    // read of the merge (m, l of the four waves, the three other waves'
+    // blocks) is issued before any is used.
     const int q = wave * 16 + ml16;
-    float mv[4], m = -INFINITY;
+    const float mo = mw[wave * ROWS + q], lo = lw[wave * ROWS + q];
+    float mv[3], lv[3];
+    floatx4 r[3][DB];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        mv[w] = mw[w * ROWS + q];
-        m = fmaxf(m, mv[w]);
+    for (int j = 0; j < 3; ++j) {
+        const int w = j < wave ? j : j + 1;        // the j-th other wave
+        const int k = wave < w ? wave : wave - 1;  // this block's slot in wave w
+        mv[j] = mw[w * ROWS + q];
+        lv[j] = lw[w * ROWS + q];
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            r[j][d] = *reinterpret_cast<const floatx4*>(ob + ((w * (QB - 1) + k) * 16 + ml16) * L::OW + d * 16 + mg * 4);
     }
+    // the wave's own block qb = wave, from registers (static indices)
     floatx4 a[DB];
-    float l = 0.0f;
-    auto own_block = [&](int w, floatx4 (&r)[DB]) {
-        // the wave's own block qb = wave, from registers (static indices)
-        static_for<QB>([&](auto qc) {
-            constexpr int qb = decltype(qc)::value;
-            if (w == qb) {
+    static_for<QB>([&](auto qc) {
+        constexpr int qb = decltype(qc)::value;
+        if (wave == qb) {
 #pragma unroll
-                for (int d = 0; d < DB; ++d) r[d] = oacc[d][qb];
-            }
-        });
-    };
-#pragma unroll
-    for (int d = 0; d < DB; ++d) a[d] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const float sc = mv[w] == -INFINITY ? 0.0f : fast_exp2(mv[w] - m);
-        l += sc * lw[w * ROWS + q];
-        if (w == wave) {
-            floatx4 r[DB];
-            own_block(w, r);
-#pragma unroll
-            for (int d = 0; d < DB; ++d) a[d] += sc * r[d];
-        } else {
-            const int k = wave < w ? wave : wave - 1;  // this block's slot in wave w
-#pragma unroll
-            for (int d = 0; d < DB; ++d)
-                a[d] += sc * *reinterpret_cast<const floatx4*>(ob + ((w * (QB - 1) + k) * 16 + ml16) * L::OW + d * 16 + mg * 4);
+            for (int d = 0; d < DB; ++d) a[d] = oacc[d][qb];
         }
+    });
+    const float m = fmaxf(fmaxf(mo, mv[0]), fmaxf(mv[1], mv[2]));
+    const float so = mo == -INFINITY ? 0.0f : fast_exp2(mo - m);
+    float l = so * lo;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) a[d] *= so;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const float sc = mv[j] == -INFINITY ? 0.0f : fast_exp2(mv[j] - m);
+        l += sc * lv[j];
+#pragma unroll
+        for (int d = 0; d < DB; ++d) a[d] += sc * r[j][d];
     }
     const int row = R0 + q;
     const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
