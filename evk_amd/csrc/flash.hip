@@ -1446,7 +1446,17 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_kvq(FlashArgs p, float* part
         }
         bwd_kv_body<DH, CAUSAL>(p, part_ws, parts_per_batch, blk, lds);
     } else {
-        bwd_q_body<DH, CAUSAL>(p, blockIdx.x - n_kv, lds);
+        // the same XCD assignment for the dQ tiles: XCD x takes the row tiles
+        // of batch x / (8 / B) (heavy first), so that one XCD's L2 holds the
+        // Q, dO and O rows of one batch for both kinds of workgroup
+        int blk = blockIdx.x - n_kv;
+        const int nrg = (p.N * p.H + 63) / 64;
+        const int xpb = p.B > 0 && 8 % p.B == 0 ? 8 / p.B : 0;
+        if (xpb > 0 && n_kv % 8 == 0 && nrg % xpb == 0) {
+            const int x = blk % 8, i = blk / 8;
+            blk = (i * xpb + x % xpb) * p.B + x / xpb;  // bwd_q_body: batch blk % B, tile blk / B
+        }
+        bwd_q_body<DH, CAUSAL>(p, blk, lds);
     }
 }
 
