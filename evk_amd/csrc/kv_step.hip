@@ -289,6 +289,403 @@ __global__ __launch_bounds__(KT, 1) void kv_step(KvArgs a) {
     product(h, static_cast<const f16*>(m.w_out), d, V, red, [&](int n, float s) { lg[n] = (f16)s; });
 }
 
+
+// ---------------------------------------------------------------------------
+// The step at d = 256 with hidden a multiple of 256 up to 1024 (the reference
+// caller's shape has hidden 512): the same arithmetic and roundings as
+// kv_step, reorganised so that the weight stream never stops.
+//
+// The weights are cut into units of 256 input rows x 256 output columns
+// (128 KB of fp16): Wq, Wk, Wv, Wo, the hidden/256 column blocks of W1 and
+// row blocks of W2 of each layer, then the column blocks of the LM head.  A
+// thread owns 8 columns (cg = tid % 32) and 16 consecutive rows
+// (kg = tid / 32) of a unit: 16 loads of 16 bytes, one 512-byte row per half
+// wave and load.  Two register slots alternate: the next unit's loads are
+// requested before the current unit is multiplied, so one unit is always in
+// flight, also across the attention, the norms and the barriers (one
+// workgroup streams about 110 GB/s from L2 with 64 KB or more in flight).
+// A unit's row partial sums cross the two half-waves by a permlane swap and
+// the eight waves in LDS, summed in wave order.  The q, k and v units share
+// one barrier, and so do the W1 blocks.  rms_norm: the threads that write x
+// also form its sum of squares (per wave, DPP), and each thread normalises
+// only the 16 rows it multiplies, in registers.
+//
+// Attention: slot = tid / 32 takes keys slot, slot + 16, ...; its 32 lanes
+// hold 8 dimensions each.  A score is a DPP sum within 16-lane rows plus a
+// permlane swap across the slot's two rows, so every lane of the slot holds
+// it.  The same slot weighs the same keys' values, so the probabilities need
+// no barrier beyond the one that publishes the slot maxima.
+// ---------------------------------------------------------------------------
+constexpr int U = 256;        // unit rows and columns; the model width
+constexpr int UPART = 8 * U;  // floats of one unit's wave partials
+
+DEV float dpp_sum_row16(float x) {
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+    return x;
+}
+// rows 0 + 1 and rows 2 + 3 (16-lane rows), the same sum in every lane of the pair
+DEV float add_row_pairs(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// lanes i and i + 32, the same sum in both
+DEV float add_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+int kv_step256_lds_floats(const evkhip_kv_model& m) { return 5 * U + 32 + (int)m.hidden + 4 * UPART + (int)m.max_seq; }
+
+__global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float kv_smem[];
+    const evkhip_kv_model& m = a.m;
+    const int hid = (int)m.hidden, V = (int)m.vocab, NL = (int)m.layers;
+    const int nh = hid / U;  // W1 column blocks = W2 row blocks
+    const int b = blockIdx.x, pos = a.pos, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int cg = tid & 31, kg = tid >> 5;  // units: 8 columns, 16 rows; attention: 8 dimensions, key slot
+    float* x = kv_smem;          // U: the residual stream
+    float* q = x + U;            // U
+    float* kk = q + U;           // U
+    float* vv = kk + U;          // U
+    float* o = vv + U;           // U
+    float* ssq = o + U;          // 8: sums of squares of x per wave (waves 0-3)
+    float* smax = ssq + 8;       // 16: score maximum per key slot
+    float* lsum = smax + 16;     // 8: probability sums per wave
+    float* u = lsum + 8;         // hid: gelu outputs
+    float* part = u + hid;       // 4 x UPART: wave partials of up to four units
+    float* sc = part + 4 * UPART;  // max_seq: scores (exp2 domain)
+
+    const auto Wl = [&](int l, int i) { return static_cast<const f16*>(m.w[l][i]); };
+    const f16* Wout = static_cast<const f16*>(m.w_out);
+    const int nvb = (V + U - 1) / U;  // LM head column blocks
+    // a unit's 16 loads through a descriptor over [base, base + bytes), rows
+    // stride_b bytes apart (the row step in the scalar offset, so one VGPR
+    // addresses all 16); lanes with !ok (the LM head's columns past the
+    // vocabulary) get an offset past any descriptor and read zeros.  No
+    // branch: the loads always go out, so the waits of the unit consumed next
+    // count them exactly.
+    const auto issue = [&](u32x4(&w)[16], const f16* base, uint32_t stride_b, uint32_t bytes, bool ok) {
+        const auto r = buf_rsrc(base, bytes);
+        const uint32_t v0 = oob_or(ok, (uint32_t)(kg * 16) * stride_b + (uint32_t)cg * 16);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = buf_load16(r, v0, (uint32_t)i * stride_b);
+        __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the work that follows
+    };
+    constexpr uint32_t UB = U * U * 2;  // bytes of a U x U matrix
+    const auto issue_lm = [&](u32x4(&w)[16], int vb) {  // LM head column block vb (zeros past the last)
+        const int c0 = min(vb, nvb) * U;
+        issue(w, Wout + c0, (uint32_t)V * 2, (uint32_t)(U * V - c0) * 2, c0 + cg * 8 < V);
+    };
+    const auto fma_unit = [&](const u32x4(&w)[16], const float(&in)[16], float(&acc)[8]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const half8 hw = as_half8(w[i]);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(in[i], (float)hw[c], acc[c]);
+        }
+    };
+    // the wave's sums of a unit's columns (its two row ranges) into part[buf]
+    const auto put_part = [&](float(&acc)[8], int buf) {
+        float r[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) r[c] = add_halves(acc[c]);
+        const float4 st = lane < 32 ? float4{r[0], r[1], r[2], r[3]} : float4{r[4], r[5], r[6], r[7]};
+        *reinterpret_cast<float4*>(part + buf * UPART + wave * U + cg * 8 + (lane >> 5) * 4) = st;
+    };
+    const auto col_sum = [&](int buf, int n) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) s += part[buf * UPART + w * U + n];
+        return s;
+    };
+    const auto lds_rows = [&](const float* src, float(&in)[16]) {
+        const float4* p = reinterpret_cast<const float4*>(src + kg * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = p[j];
+            in[4 * j] = v.x;
+            in[4 * j + 1] = v.y;
+            in[4 * j + 2] = v.z;
+            in[4 * j + 3] = v.w;
+        }
+    };
+    // threads 0..U-1 (waves 0-3), v = x[tid]: ssq[wave] = sum of clamp(x)^2 over the wave
+    const auto sumsq_store = [&](float v) {
+        const float c = fminf(fmaxf(v, -65504.0f), 65504.0f);
+        const float s = add_halves(add_row_pairs(dpp_sum_row16(c * c)));
+        if (lane == 0) ssq[wave] = s;
+    };
+    // h = fp16(clamp(x) / sqrt(mean(clamp(x)^2) + eps)) of this thread's 16 rows, as rms_norm_k
+    float hr[16];
+    const auto norm_rows = [&]() {
+        const float inv = 1.0f / sqrtf((ssq[0] + ssq[1] + ssq[2] + ssq[3]) / (float)U + m.eps);
+        float xr[16];
+        lds_rows(x, xr);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) hr[i] = rnd16(fminf(fmaxf(xr[i], -65504.0f), 65504.0f) * inv);
+    };
+
+    u32x4 wa[16], wb[16];
+    issue(wa, Wl(0, 0), 2 * U, UB, true);
+    // rope angles of this position: threads 0..U-1 take pair tid % (U / 2)
+    float rc = 1.0f, rs = 0.0f;
+    if (tid < U) {
+        const int pr = tid & (U / 2 - 1);
+        const float inv_freq = powf(m.rope_base, -2.0f * (float)pr / (float)U);
+        sincosf((float)pos * inv_freq, &rs, &rc);
+        const int tok = min((int)a.ids[b], V - 1);
+        const float v = (float)static_cast<const f16*>(m.emb)[(int64_t)tok * U + tid];
+        x[tid] = v;
+        sumsq_store(v);
+    }
+    __syncthreads();
+    const float scale_log2 = 1.4426950408889634f / sqrtf((float)U);
+
+    for (int l = 0; l < NL; ++l) {
+        f16* Kc = static_cast<f16*>(m.k_cache[l]) + (int64_t)b * m.max_seq * U;
+        f16* Vc = static_cast<f16*>(m.v_cache[l]) + (int64_t)b * m.max_seq * U;
+        norm_rows();
+        float acc[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        issue(wb, Wl(l, 1), 2 * U, UB, true);
+        fma_unit(wa, hr, acc);
+        put_part(acc, 0);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        issue(wa, Wl(l, 2), 2 * U, UB, true);
+        fma_unit(wb, hr, acc);
+        put_part(acc, 1);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        issue(wb, Wl(l, 3), 2 * U, UB, true);
+        fma_unit(wa, hr, acc);
+        put_part(acc, 2);
+        __syncthreads();
+        // q, k = rope(fp16(h Wq)), rope(fp16(h Wk)) (threads 0..127 q pairs,
+        // 128..255 k pairs), v = fp16(h Wv); the cache rows of this position
+        if (tid < U) {
+            const int pr = tid & (U / 2 - 1);
+            const float* pp = part + (tid < U / 2 ? 0 : UPART) + 2 * pr;
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const float2 t = *reinterpret_cast<const float2*>(pp + w * U);
+                s0 += t.x;
+                s1 += t.y;
+            }
+            const float a0 = rnd16(s0), a1 = rnd16(s1);
+            const float r0 = a0 * rc - a1 * rs, r1 = a0 * rs + a1 * rc;
+            if (tid < U / 2) {
+                q[2 * pr] = rnd16(r0);
+                q[2 * pr + 1] = rnd16(r1);
+            } else {
+                const f16 k0 = (f16)r0, k1 = (f16)r1;
+                *reinterpret_cast<uint32_t*>(Kc + (int64_t)pos * U + 2 * pr) =
+                    (uint32_t)__builtin_bit_cast(uint16_t, k0) | ((uint32_t)__builtin_bit_cast(uint16_t, k1) << 16);
+                kk[2 * pr] = (float)k0;
+                kk[2 * pr + 1] = (float)k1;
+            }
+        } else {
+            const int n = tid - U;
+            const float v = rnd16(col_sum(2, n));
+            vv[n] = v;
+            Vc[(int64_t)pos * U + n] = (f16)v;
+        }
+        __syncthreads();
+
+        // scores of keys [0, pos] (the row at pos is this step's k, from LDS);
+        // eight keys' loads go out before any is used
+        float qv[8];
+        {
+            const float4 q0 = *reinterpret_cast<const float4*>(q + cg * 8);
+            const float4 q1 = *reinterpret_cast<const float4*>(q + cg * 8 + 4);
+            qv[0] = q0.x, qv[1] = q0.y, qv[2] = q0.z, qv[3] = q0.w;
+            qv[4] = q1.x, qv[5] = q1.y, qv[6] = q1.z, qv[7] = q1.w;
+        }
+        // descriptors over the cache rows [0, pos): rows at and past pos read zeros
+        const auto rK = buf_rsrc(Kc, (uint32_t)pos * U * 2), rV = buf_rsrc(Vc, (uint32_t)pos * U * 2);
+        // keys j < pos from the cache (slot kg: kg, kg + 16, ...); key pos is
+        // the last key of slot pos % 16 and is added after them
+        float mloc = -INFINITY;
+        for (int j0 = 0; j0 < pos; j0 += 16 * KB) {
+            half8 kv8[KB];
+#pragma unroll
+            for (int t = 0; t < KB; ++t)
+                kv8[t] = as_half8(buf_load16(rK, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
+            float sv[KB];
+#pragma unroll
+            for (int t = 0; t < KB; ++t) {
+                float d = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kv8[t][c], d);
+                sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
+            }
+#pragma unroll
+            for (int t = 0; t < KB; ++t) {
+                const int j = j0 + kg + 16 * t;
+                mloc = j < pos ? fmaxf(mloc, sv[t]) : mloc;
+                if (cg == t && j < pos) sc[j] = sv[t];
+            }
+        }
+        {
+            const float4 k0 = *reinterpret_cast<const float4*>(kk + cg * 8);
+            const float4 k1 = *reinterpret_cast<const float4*>(kk + cg * 8 + 4);
+            const float kr[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], kr[c], d);
+            const float s2 = add_row_pairs(dpp_sum_row16(d)) * scale_log2;  // the same in every slot
+            if (kg == (pos & 15)) {
+                mloc = fmaxf(mloc, s2);
+                if (cg == 0) sc[pos] = s2;
+            }
+        }
+        if (cg == 0) smax[kg] = mloc;
+        __syncthreads();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 t = *reinterpret_cast<const float4*>(smax + 4 * j);
+            mx = fmaxf(mx, fmaxf(fmaxf(t.x, t.y), fmaxf(t.z, t.w)));
+        }
+        // P V over the slot's keys (the ones whose scores it wrote)
+        float lp = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        for (int j0 = 0; j0 < pos; j0 += 16 * KB) {
+            half8 v8[KB];
+#pragma unroll
+            for (int t = 0; t < KB; ++t)
+                v8[t] = as_half8(buf_load16(rV, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
+#pragma unroll
+            for (int t = 0; t < KB; ++t) {
+                const int j = j0 + kg + 16 * t;
+                if (j < pos) {
+                    const float p = exp2f(sc[j] - mx);
+                    lp += p;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(p, (float)v8[t][c], acc[c]);
+                }
+            }
+        }
+        if (kg == (pos & 15)) {
+            const float p = exp2f(sc[pos] - mx);
+            lp += p;
+            const float4 v0 = *reinterpret_cast<const float4*>(vv + cg * 8);
+            const float4 v1 = *reinterpret_cast<const float4*>(vv + cg * 8 + 4);
+            const float vr[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(p, vr[c], acc[c]);
+        }
+        put_part(acc, 0);
+        lp = add_halves(lp);
+        if (lane == 0) lsum[wave] = lp;
+        __syncthreads();
+        if (tid < U) {
+            float lt = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) lt += lsum[w];
+            o[tid] = rnd16(col_sum(0, tid) * (1.0f / lt));
+        }
+        __syncthreads();
+
+        // x = x + fp16(o Wo); the first W1 block goes out
+        {
+            float in[16];
+            lds_rows(o, in);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+            issue(wa, Wl(l, 4), (uint32_t)hid * 2, (uint32_t)(U * hid) * 2, true);
+            fma_unit(wb, in, acc);
+            put_part(acc, 1);
+        }
+        __syncthreads();
+        if (tid < U) {
+            const float v = rnd16(x[tid] + rnd16(col_sum(1, tid)));
+            x[tid] = v;
+            sumsq_store(v);
+        }
+        __syncthreads();
+        norm_rows();
+
+        // MLP units t = 0 .. 2 nh - 1: W1 column block t (t < nh), then W2
+        // row block t - nh; unit t sits in slot wa for even t.  After them
+        // comes the next layer's Wq or the LM head's first block.
+        float acc2[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc2[c] = 0.0f;
+        const auto next_unit = [&](u32x4(&w)[16], int t) {  // selects only: one issue site
+            const bool w1 = t < nh, w2 = !w1 && t < 2 * nh, lm = t >= 2 * nh && l + 1 == NL;
+            const f16* base = w1   ? Wl(l, 4) + t * U
+                              : w2 ? Wl(l, 5) + (int64_t)(t - nh) * U * U
+                              : lm ? Wout
+                                   : Wl(l + 1, 0);
+            const uint32_t stride_b = w1 ? (uint32_t)hid * 2 : lm ? (uint32_t)V * 2 : 2 * U;
+            const uint32_t bytes = w1 ? (uint32_t)(U * hid - t * U) * 2 : lm ? (uint32_t)(U * V) * 2 : UB;
+            issue(w, base, stride_b, bytes, !lm || cg * 8 < V);
+        };
+        const auto consume_mlp = [&](const u32x4(&w)[16], int t) {
+            if (t < nh) {
+                float a1[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) a1[c] = 0.0f;
+                fma_unit(w, hr, a1);
+                put_part(a1, t);
+                if (t == nh - 1) {
+                    __syncthreads();
+                    for (int n = tid; n < hid; n += KT) u[n] = rnd16(gelu_f(rnd16(col_sum(n / U, n % U))));
+                    __syncthreads();
+                }
+            } else {
+                float in[16];
+                lds_rows(u + (t - nh) * U, in);
+                fma_unit(w, in, acc2);
+                if (t == 2 * nh - 1) {
+                    put_part(acc2, 0);
+                    __syncthreads();
+                    if (tid < U) {
+                        const float v = rnd16(x[tid] + rnd16(col_sum(0, tid)));
+                        x[tid] = v;
+                        sumsq_store(v);
+                    }
+                    __syncthreads();
+                }
+            }
+        };
+        for (int t = 0; t < 2 * nh; t += 2) {
+            next_unit(wb, t + 1);
+            consume_mlp(wa, t);
+            next_unit(wa, t + 2);
+            consume_mlp(wb, t + 1);
+        }
+    }
+
+    // logits = fp16(rms_norm(x) Wout), column blocks of U; block vb sits in
+    // slot wa for even vb
+    norm_rows();
+    f16* lg = a.logits + (int64_t)b * V;
+    const auto lm_block = [&](const u32x4(&w)[16], int vb) {
+        float a1[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) a1[c] = 0.0f;
+        fma_unit(w, hr, a1);
+        put_part(a1, vb & 1);
+        __syncthreads();
+        if (tid < U && vb * U + tid < V) lg[vb * U + tid] = (f16)col_sum(vb & 1, tid);
+    };
+    for (int vb = 0; vb < nvb; vb += 2) {  // an odd count ends with a block of zeros, not stored
+        issue_lm(wb, vb + 1);
+        lm_block(wa, vb);
+        issue_lm(wa, vb + 2);
+        lm_block(wb, vb + 1);
+    }
+}
+
 }  // namespace
 
 int kv_step_lds_bytes(const evkhip_kv_model& m) {
@@ -327,7 +724,9 @@ extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* i
         al = al && aligned16(m->k_cache[l]) && aligned16(m->v_cache[l]);
     }
     EVK_RETURN_IF(!al, EVKHIP_ERR_UNSUPPORTED, "kv_decode_step: needs 16-byte aligned weights and caches");
-    const int lds = kv_step_lds_bytes(*m);
+    // d = 256 with hidden a multiple of 256 up to 1024: the streamed step
+    const bool units = m->d == U && m->hidden % U == 0 && m->hidden <= 4 * U;
+    const int lds = units ? kv_step256_lds_floats(*m) * (int)sizeof(float) : kv_step_lds_bytes(*m);
     int dev = 0, lds_max = 0;
     EVK_HIP(hipGetDevice(&dev));
     EVK_HIP(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
@@ -338,7 +737,8 @@ extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* i
     a.ids = ids;
     a.pos = (int)pos;
     a.logits = static_cast<f16*>(logits);
-    hipLaunchKernelGGL(kv_step, dim3(m->batch), dim3(KT), (unsigned)lds, reinterpret_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(units ? kv_step256 : kv_step, dim3(m->batch), dim3(KT), (unsigned)lds,
+                       reinterpret_cast<hipStream_t>(stream), a);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? EVKHIP_OK : check_hip(e, "kv_decode_step launch");
 }

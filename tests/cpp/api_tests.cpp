@@ -943,6 +943,66 @@ static void test_kv_decoder_matches_full_recompute() {
     TEST(max_dlogit < 1e-2f);
 }
 
+// The fused one-launch decode step (evkhip_kv_decode_step) against the
+// op-by-op step, in lockstep over the same ids, at shapes other than the
+// reference caller's: d = 256 with hidden 768 (three W1/W2 blocks), a
+// vocabulary of three LM-head blocks and positions past 128 keys (several
+// attention passes) for the streamed d = 256 kernel, and d = 128 for the
+// general kernel.  The op-by-op step's ops are each checked against the CPU
+// oracle; the two steps differ only in summation order.
+static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint32_t L, uint32_t V, uint32_t S,
+                                      uint32_t prefix, uint32_t steps) {
+    std::printf("test_kv_fused_vs_op_by_op(B=%u, D=%u, hidden=%u, layers=%u, vocab=%u, max_seq=%u)\n", B, D, HID, L,
+                V, S);
+    srand(1234 + D + HID);
+    Tensor emb({V, D}), w_out({D, V});
+    emb.random_init(0.5f);
+    w_out.random_init(0.05f);
+    std::vector<std::unique_ptr<Tensor>> keep;
+    std::vector<evk::ai::DecoderLayer> layers(L);
+    auto mk = [&](uint32_t r, uint32_t c, float sd) {
+        keep.emplace_back(std::make_unique<Tensor>(Shape({r, c})));
+        return &keep.back()->random_init(sd);
+    };
+    for (uint32_t l = 0; l < L; ++l) {
+        evk::ai::DecoderLayer& w = layers[l];
+        w.w_q = mk(D, D, 0.08f);
+        w.w_k = mk(D, D, 0.08f);
+        w.w_v = mk(D, D, 0.05f);
+        w.w_o = mk(D, D, 0.05f);
+        w.w1 = mk(D, HID, 0.05f);
+        w.w2 = mk(HID, D, 0.05f);
+    }
+    evk::ai::KVCacheDecoder dec(emb, w_out, layers, B, S);
+    evk::ai::KVCacheDecoder dec_ops(emb, w_out, layers, B, S);
+    dec_ops.set_fused(false);
+    Lcg rng(99);
+    auto rand_ids = [&](Tensor& t) {
+        float16_t* h = t.cpu();
+        for (uint32_t i = 0; i < t.shape.count(); ++i) h[i].value = uint16_t(uint32_t((rng.uniform() + 1.0f) * 0.5f * V) % V);
+        t.cpu_upload();
+    };
+    Tensor prompt({B, prefix}), ids({B});
+    rand_ids(prompt);
+    dec.prefill(prompt);
+    dec_ops.prefill(prompt);
+    float worst = 0.0f, mag = 0.0f;
+    for (uint32_t s = 0; s < steps; ++s) {
+        rand_ids(ids);
+        const std::vector<float> f = download(dec.step(ids));
+        const std::vector<float> o = download(dec_ops.step(ids));
+        for (size_t i = 0; i < f.size(); ++i) {
+            worst = std::fmax(worst, std::fabs(f[i] - o[i]));
+            mag = std::fmax(mag, std::fabs(o[i]));
+        }
+    }
+    std::printf("  %u steps from position %u: max |fused - op-by-op| %.4g (max |logit| %.4g)\n", steps, prefix,
+                worst, mag);
+    TEST(dec.cached() == prefix + steps);
+    TEST(mag > 0.1f);
+    TEST(worst < 1e-2f);
+}
+
 static void test_timestamps() {
     std::printf("test_timestamps()\n");
     const uint32_t n = 1024;
@@ -1027,6 +1087,8 @@ int main(int argc, char** argv) {
     test_graph_causal_attention_fused_vs_unfused(16, 160, 256);
     test_graph_tiny_lm();
     test_kv_decoder_matches_full_recompute();
+    test_kv_fused_vs_op_by_op(3, 256, 768, 2, 600, 300, 120, 24);
+    test_kv_fused_vs_op_by_op(2, 128, 256, 2, 200, 64, 9, 8);
     test_timestamps();
     evk::ai::shutdown();
     std::printf("ALL PASSED\n");
