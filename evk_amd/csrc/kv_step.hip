@@ -313,11 +313,14 @@ __global__ __launch_bounds__(KT, 1) void kv_step(KvArgs a) {
 // Attention: slot = tid / 32 takes keys slot, slot + 16, ...; its 32 lanes
 // hold 8 dimensions each.  A score is a DPP sum within 16-lane rows plus a
 // permlane swap across the slot's two rows, so every lane of the slot holds
-// it.  The same slot weighs the same keys' values, so the probabilities need
-// no barrier beyond the one that publishes the slot maxima.
+// it.  Each slot runs an online softmax over its keys, four keys a pass with
+// their K and V rows requested together (the first pass's before the v unit
+// is multiplied, ahead of Wo, so they do not queue behind it); the two slots
+// of a wave merge by a permlane swap and the eight waves in one LDS pass.
 // ---------------------------------------------------------------------------
 constexpr int U = 256;        // unit rows and columns; the model width
 constexpr int UPART = 8 * U;  // floats of one unit's wave partials
+constexpr int KB4 = 4;        // keys of a slot per attention pass
 
 DEV float dpp_sum_row16(float x) {
     x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
@@ -337,7 +340,7 @@ DEV float add_halves(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-int kv_step256_lds_floats(const evkhip_kv_model& m) { return 5 * U + 32 + (int)m.hidden + 4 * UPART + (int)m.max_seq; }
+int kv_step256_lds_floats(const evkhip_kv_model& m) { return 5 * U + 32 + (int)m.hidden + 4 * UPART; }
 
 __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float kv_smem[];
@@ -353,11 +356,10 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
     float* vv = kk + U;          // U
     float* o = vv + U;           // U
     float* ssq = o + U;          // 8: sums of squares of x per wave (waves 0-3)
-    float* smax = ssq + 8;       // 16: score maximum per key slot
-    float* lsum = smax + 16;     // 8: probability sums per wave
+    float* smax = ssq + 8;       // 16: the attention's running maximum per wave (8 used)
+    float* lsum = smax + 16;     // 8: the attention's probability sum per wave
     float* u = lsum + 8;         // hid: gelu outputs
     float* part = u + hid;       // 4 x UPART: wave partials of up to four units
-    float* sc = part + 4 * UPART;  // max_seq: scores (exp2 domain)
 
     const auto Wl = [&](int l, int i) { return static_cast<const f16*>(m.w[l][i]); };
     const f16* Wout = static_cast<const f16*>(m.w_out);
@@ -446,8 +448,11 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
     const float scale_log2 = 1.4426950408889634f / sqrtf((float)U);
 
     for (int l = 0; l < NL; ++l) {
-        f16* Kc = static_cast<f16*>(m.k_cache[l]) + (int64_t)b * m.max_seq * U;
-        f16* Vc = static_cast<f16*>(m.v_cache[l]) + (int64_t)b * m.max_seq * U;
+        // this sequence's cache rows; the offset is formed in scalar registers
+        // so that the descriptors below need no per-lane loop
+        const uint64_t seq_off = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(b * (int)m.max_seq) * U;
+        f16* Kc = static_cast<f16*>(m.k_cache[l]) + seq_off;
+        f16* Vc = static_cast<f16*>(m.v_cache[l]) + seq_off;
         norm_rows();
         float acc[8];
 #pragma unroll
@@ -462,8 +467,19 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
         put_part(acc, 1);
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
-        issue(wb, Wl(l, 3), 2 * U, UB, true);
+        // the attention's first keys and values (cache rows, independent of
+        // this step) go out before the v unit is multiplied, Wo after it, so
+        // that they do not queue behind Wo.  Descriptors over the rows
+        // [0, pos): rows at and past pos read zeros.
+        const auto rK = buf_rsrc(Kc, (uint32_t)pos * U * 2), rV = buf_rsrc(Vc, (uint32_t)pos * U * 2);
+        half8 kp[KB4], vp[KB4];
+#pragma unroll
+        for (int t = 0; t < KB4; ++t) {
+            kp[t] = as_half8(buf_load16(rK, (uint32_t)((kg + 16 * t) * U + cg * 8) * 2, 0));
+            vp[t] = as_half8(buf_load16(rV, (uint32_t)((kg + 16 * t) * U + cg * 8) * 2, 0));
+        }
         fma_unit(wa, hr, acc);
+        issue(wb, Wl(l, 3), 2 * U, UB, true);
         put_part(acc, 2);
         __syncthreads();
         // q, k = rope(fp16(h Wq)), rope(fp16(h Wk)) (threads 0..127 q pairs,
@@ -498,8 +514,11 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
         }
         __syncthreads();
 
-        // scores of keys [0, pos] (the row at pos is this step's k, from LDS);
-        // eight keys' loads go out before any is used
+        // attention: each key slot runs an online softmax over its keys
+        // kg, kg + 16, ... (KB4 keys a pass, K and V rows requested together),
+        // the slots of a wave merge by a permlane swap and the waves in LDS.
+        // Key pos (this step's k and v, from LDS) is the last key of slot
+        // pos % 16.
         float qv[8];
         {
             const float4 q0 = *reinterpret_cast<const float4*>(q + cg * 8);
@@ -507,30 +526,43 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
             qv[0] = q0.x, qv[1] = q0.y, qv[2] = q0.z, qv[3] = q0.w;
             qv[4] = q1.x, qv[5] = q1.y, qv[6] = q1.z, qv[7] = q1.w;
         }
-        // descriptors over the cache rows [0, pos): rows at and past pos read zeros
-        const auto rK = buf_rsrc(Kc, (uint32_t)pos * U * 2), rV = buf_rsrc(Vc, (uint32_t)pos * U * 2);
-        // keys j < pos from the cache (slot kg: kg, kg + 16, ...); key pos is
-        // the last key of slot pos % 16 and is added after them
-        float mloc = -INFINITY;
-        for (int j0 = 0; j0 < pos; j0 += 16 * KB) {
-            half8 kv8[KB];
+        float m_run = -INFINITY, l_run = 0.0f;
 #pragma unroll
-            for (int t = 0; t < KB; ++t)
-                kv8[t] = as_half8(buf_load16(rK, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
-            float sv[KB];
+        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+        // keys j0 + kg + 16 t (t < KB4) that are below pos
+        const auto absorb = [&](const half8(&kx)[KB4], const half8(&vx)[KB4], int j0) {
+            float sv[KB4];
+            float mn = m_run;
 #pragma unroll
-            for (int t = 0; t < KB; ++t) {
+            for (int t = 0; t < KB4; ++t) {
                 float d = 0.0f;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kv8[t][c], d);
+                for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kx[t][c], d);
                 sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
+                mn = j0 + kg + 16 * t < pos ? fmaxf(mn, sv[t]) : mn;
             }
+            const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
+            l_run *= f;
 #pragma unroll
-            for (int t = 0; t < KB; ++t) {
-                const int j = j0 + kg + 16 * t;
-                mloc = j < pos ? fmaxf(mloc, sv[t]) : mloc;
-                if (cg == t && j < pos) sc[j] = sv[t];
+            for (int c = 0; c < 8; ++c) acc[c] *= f;
+#pragma unroll
+            for (int t = 0; t < KB4; ++t)
+                if (j0 + kg + 16 * t < pos) {
+                    const float pr = exp2f(sv[t] - mn);
+                    l_run += pr;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, (float)vx[t][c], acc[c]);
+                }
+            m_run = mn;
+        };
+        absorb(kp, vp, 0);
+        for (int j0 = 16 * KB4; j0 < pos; j0 += 16 * KB4) {
+#pragma unroll
+            for (int t = 0; t < KB4; ++t) {
+                kp[t] = as_half8(buf_load16(rK, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
+                vp[t] = as_half8(buf_load16(rV, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
             }
+            absorb(kp, vp, j0);
         }
         {
             const float4 k0 = *reinterpret_cast<const float4*>(kk + cg * 8);
@@ -541,56 +573,51 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
             for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], kr[c], d);
             const float s2 = add_row_pairs(dpp_sum_row16(d)) * scale_log2;  // the same in every slot
             if (kg == (pos & 15)) {
-                mloc = fmaxf(mloc, s2);
-                if (cg == 0) sc[pos] = s2;
+                const float mn = fmaxf(m_run, s2);
+                const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn), pr = exp2f(s2 - mn);
+                const float4 v0 = *reinterpret_cast<const float4*>(vv + cg * 8);
+                const float4 v1 = *reinterpret_cast<const float4*>(vv + cg * 8 + 4);
+                const float vr[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                l_run = l_run * f + pr;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, vr[c], acc[c] * f);
+                m_run = mn;
             }
         }
-        if (cg == 0) smax[kg] = mloc;
-        __syncthreads();
-        float mx = -INFINITY;
+        // the wave's two slots (lanes 0-31 and 32-63)
+        {
+            const auto rm = __builtin_amdgcn_permlane32_swap(__float_as_uint(m_run), __float_as_uint(m_run), false, false);
+            const float m_lo = __uint_as_float(rm[0]), m_hi = __uint_as_float(rm[1]), mw = fmaxf(m_lo, m_hi);
+            const float f_lo = m_lo == -INFINITY ? 0.0f : exp2f(m_lo - mw);
+            const float f_hi = m_hi == -INFINITY ? 0.0f : exp2f(m_hi - mw);
+            float r[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float4 t = *reinterpret_cast<const float4*>(smax + 4 * j);
-            mx = fmaxf(mx, fmaxf(fmaxf(t.x, t.y), fmaxf(t.z, t.w)));
-        }
-        // P V over the slot's keys (the ones whose scores it wrote)
-        float lp = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
-        for (int j0 = 0; j0 < pos; j0 += 16 * KB) {
-            half8 v8[KB];
-#pragma unroll
-            for (int t = 0; t < KB; ++t)
-                v8[t] = as_half8(buf_load16(rV, (uint32_t)((j0 + kg + 16 * t) * U + cg * 8) * 2, 0));
-#pragma unroll
-            for (int t = 0; t < KB; ++t) {
-                const int j = j0 + kg + 16 * t;
-                if (j < pos) {
-                    const float p = exp2f(sc[j] - mx);
-                    lp += p;
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(p, (float)v8[t][c], acc[c]);
-                }
+            for (int c = 0; c < 8; ++c) {
+                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[c]), __float_as_uint(acc[c]), false, false);
+                r[c] = __uint_as_float(t[0]) * f_lo + __uint_as_float(t[1]) * f_hi;
+            }
+            const auto rl = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+            const float lw = __uint_as_float(rl[0]) * f_lo + __uint_as_float(rl[1]) * f_hi;
+            const float4 st = lane < 32 ? float4{r[0], r[1], r[2], r[3]} : float4{r[4], r[5], r[6], r[7]};
+            *reinterpret_cast<float4*>(part + wave * U + cg * 8 + (lane >> 5) * 4) = st;
+            if (lane == 0) {
+                smax[wave] = mw;
+                lsum[wave] = lw;
             }
         }
-        if (kg == (pos & 15)) {
-            const float p = exp2f(sc[pos] - mx);
-            lp += p;
-            const float4 v0 = *reinterpret_cast<const float4*>(vv + cg * 8);
-            const float4 v1 = *reinterpret_cast<const float4*>(vv + cg * 8 + 4);
-            const float vr[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-            for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(p, vr[c], acc[c]);
-        }
-        put_part(acc, 0);
-        lp = add_halves(lp);
-        if (lane == 0) lsum[wave] = lp;
         __syncthreads();
         if (tid < U) {
-            float lt = 0.0f;
+            float M = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < 8; ++w) lt += lsum[w];
-            o[tid] = rnd16(col_sum(0, tid) * (1.0f / lt));
+            for (int w = 0; w < 8; ++w) M = fmaxf(M, smax[w]);
+            float num = 0.0f, den = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const float f = smax[w] == -INFINITY ? 0.0f : exp2f(smax[w] - M);
+                num = __builtin_fmaf(part[w * U + tid], f, num);
+                den = __builtin_fmaf(lsum[w], f, den);
+            }
+            o[tid] = rnd16(num * (1.0f / den));
         }
         __syncthreads();
 
