@@ -63,16 +63,17 @@ constexpr int YO = 144;            // stage output floats (>= head rows per slot
 __device__ unsigned g_dec_status;
 
 #ifdef EVKHIP_DECODE_TRACE
-// Stage timestamps of one step and layer (a separate trace build of the
-// library, evk_amd/build.py --decode-trace): per workgroup and stage kind
-// S1..S5, the 100 MHz wall clock when the stage starts, when its input has
-// arrived and when its outputs are stored.
-constexpr int kTraceStep = 3, kTraceLayer = 2;
-__device__ unsigned long long g_dec_trace[1024][5][3];
-#define DEC_TRACE(c, i)                                                                                 \
-    do {                                                                                                \
-        if (threadIdx.x == 0 && (c).t == kTraceStep && (c).l == kTraceLayer && (c).k < K_HEAD)          \
-            g_dec_trace[blockIdx.x][(c).k][(i)] = __builtin_amdgcn_s_memrealtime();                     \
+// Stage timestamps of one step and two consecutive layers (a separate trace
+// build of the library, evk_amd/build.py --decode-trace): per layer,
+// workgroup and stage kind S1..S5, the 100 MHz wall clock when the stage
+// starts, when its input has arrived and when its outputs are stored.
+constexpr int kTraceStep = 3, kTraceLayer = 2;  // layers kTraceLayer - 1 and kTraceLayer
+__device__ unsigned long long g_dec_trace[2][1024][5][3];
+#define DEC_TRACE(c, i)                                                                                     \
+    do {                                                                                                    \
+        if (threadIdx.x == 0 && (c).t == kTraceStep && ((c).l == kTraceLayer || (c).l == kTraceLayer - 1) && \
+            (c).k < K_HEAD)                                                                                 \
+            g_dec_trace[(c).l - kTraceLayer + 1][blockIdx.x][(c).k][(i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define DEC_TRACE(c, i) \
@@ -1206,7 +1207,7 @@ int evkhip_debug_decode_set_epoch(uint32_t distance) {
 }
 
 #ifdef EVKHIP_DECODE_TRACE
-// The trace of the last launch (trace build only): 1024 x 5 x 3 uint64.
+// The trace of the last launch (trace build only): 2 x 1024 x 5 x 3 uint64.
 int evkhip_debug_decode_trace(void* dst) {
     return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_dec_trace), sizeof(g_dec_trace), 0, hipMemcpyDeviceToHost) ==
                    hipSuccess

@@ -10,7 +10,8 @@ stage (S1 rms_norm+QKV+rope, S2 attention splits, S3 split merge+Wo+residual,
 S4 rms_norm+W1+gelu, S5 W2+residual): how many workgroups take part, when
 they start, when their input has arrived and when their outputs are stored
 (100 MHz wall clock, microseconds from the layer's first start), and per
-workgroup the wait for the input and the time from input to stored output.
+workgroup the wait for the input and the time from input to stored output;
+then the hand-over into the layer, from layer 1's last S5 store.
 """
 import ctypes as C
 import os
@@ -61,12 +62,14 @@ def main():
     assert evk.device_status(clear=True) == 0, "the persistent decode reported a wait timeout"
     L = evk.lib()
     L.evkhip_debug_decode_trace.argtypes = [C.c_void_p]
-    buf = np.zeros((1024, 5, 3), np.uint64)
+    buf = np.zeros((2, 1024, 5, 3), np.uint64)
     assert L.evkhip_debug_decode_trace(buf.ctypes.data) == 0
-    t = buf.astype(np.int64)
+    tt = buf.astype(np.int64)
+    t, tprev = tt[1], tt[0]  # layer 2, layer 1
     took = t[:, :, 0] > 0
     t0 = t[:, 0, 0][took[:, 0]].min()
     us = (t - t0) * 0.01  # 100 MHz ticks -> us
+    us_prev = (tprev - t0) * 0.01
     names = ["S1 rms_norm+QKV+rope", "S2 attention splits", "S3 merge+Wo+residual", "S4 rms_norm+W1+gelu",
              "S5 W2+residual"]
     print(f"# persistent decode stage timeline, C4 model (12 layers, d=768), step 3 of 8 (position 1027), layer 2")
@@ -86,6 +89,24 @@ def main():
               f"{c.max():9.2f} {med(b - a):9.2f} {med(c - b):9.2f} {(c - b).max():9.2f}")
     last = us[took[:, 4], 4, 2].max()
     print(f"# layer span (first S1 start to last S5 store): {last:.2f} us")
+    took_prev = tprev[:, 4, 0] > 0
+    if took_prev.any():
+        prev_done = us_prev[took_prev, 4, 2].max()
+        s1_in = float(np.median(us[took[:, 0], 0, 1]))
+        print(f"# hop into the layer: layer 1's last S5 store at {prev_done:.2f} us, layer 2's S1 input (median) "
+              f"at {s1_in:.2f} us: {s1_in - prev_done:.2f} us")
+        # the chain from layer 1's last S5 store to layer 2's: per stage the hand-over (the producers' last
+        # store to the consumers' median input) and the work (median input to the last store)
+        hops, work, done = [], [], prev_done
+        for k in range(5):
+            sel = took[:, k]
+            inp = float(np.median(us[sel, k, 1]))
+            hops.append(inp - done)
+            done = us[sel, k, 2].max()
+            work.append(done - inp)
+        print(f"# layer 2 from layer 1's last S5 store: {done - prev_done:.2f} us = hand-overs "
+              f"{' + '.join(f'{h:.2f}' for h in hops)} = {sum(hops):.2f} us, stage work "
+              f"{' + '.join(f'{w:.2f}' for w in work)} = {sum(work):.2f} us")
 
 
 if __name__ == "__main__":
