@@ -358,7 +358,10 @@ int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* 
  * raw uint16 token ids of position pos.  Needs d, hidden, vocab multiples of
  * 8 (d <= 2048, hidden <= 8192), max_seq <= 8192, at most
  * EVKHIP_KV_MAX_LAYERS layers and 16-byte aligned pointers, else
- * EVKHIP_ERR_UNSUPPORTED (the op-by-op step serves those shapes). */
+ * EVKHIP_ERR_UNSUPPORTED (the op-by-op step serves those shapes).  d = 256
+ * with hidden a multiple of 256 up to 1024 (the reference caller's shape)
+ * takes a kernel that streams the weights with loads always in flight;
+ * other shapes a general one.  The two sum in different orders. */
 #define EVKHIP_KV_MAX_LAYERS 24
 typedef struct evkhip_kv_model {
     uint32_t batch, d, hidden, vocab, layers, max_seq;
