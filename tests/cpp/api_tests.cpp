@@ -945,10 +945,10 @@ static void test_kv_decoder_matches_full_recompute() {
 
 // The fused one-launch decode step (evkhip_kv_decode_step) against the
 // op-by-op step, in lockstep over the same ids, at shapes other than the
-// reference caller's: d = 256 with hidden 768 (three W1/W2 blocks), a
-// vocabulary of three LM-head blocks and positions past 128 keys (several
-// attention passes) for the streamed d = 256 kernel, and d = 128 for the
-// general kernel.  The op-by-op step's ops are each checked against the CPU
+// reference caller's: for the streamed d = 256 kernel hidden 256, 768 and
+// 1024 (one, three and four W1/W2 blocks), vocabularies of one to three
+// LM-head blocks and positions up to 201 (up to four attention passes of 64
+// keys); d = 128 for the general kernel.  The op-by-op step's ops are each checked against the CPU
 // oracle; the two steps differ only in summation order.
 static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint32_t L, uint32_t V, uint32_t S,
                                       uint32_t prefix, uint32_t steps) {
@@ -1088,6 +1088,11 @@ int main(int argc, char** argv) {
     test_graph_tiny_lm();
     test_kv_decoder_matches_full_recompute();
     test_kv_fused_vs_op_by_op(3, 256, 768, 2, 600, 300, 120, 24);
+    // the streamed kernel's edges: one W1/W2 block and a vocabulary under one
+    // LM-head block; four W1/W2 blocks, two LM-head blocks and up to four
+    // attention passes
+    test_kv_fused_vs_op_by_op(2, 256, 256, 1, 72, 40, 5, 6);
+    test_kv_fused_vs_op_by_op(1, 256, 1024, 1, 264, 240, 190, 12);
     test_kv_fused_vs_op_by_op(2, 128, 256, 2, 200, 64, 9, 8);
     test_timestamps();
     evk::ai::shutdown();
