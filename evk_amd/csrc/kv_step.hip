@@ -289,7 +289,6 @@ __global__ __launch_bounds__(KT, 1) void kv_step(KvArgs a) {
     product(h, static_cast<const f16*>(m.w_out), d, V, red, [&](int n, float s) { lg[n] = (f16)s; });
 }
 
-
 // ---------------------------------------------------------------------------
 // The step at d = 256 with hidden a multiple of 256 up to 1024 (the reference
 // caller's shape has hidden 512): the same arithmetic and roundings as
