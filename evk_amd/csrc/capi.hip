@@ -94,6 +94,7 @@ int evkhip_shutdown(void) {
     model_free_workspace();
     decode_persist_free_workspace();
     train_ops_free_workspace();
+    kv_step_free_workspace();
     return EVKHIP_OK;
 }
 
@@ -104,7 +105,10 @@ int evkhip_device_status(uint32_t* flags, int clear) {
     if (rc != EVKHIP_OK) return rc;
     rc = decode_status(&g, clear != 0);
     if (rc != EVKHIP_OK) return rc;
-    *flags = f | g;
+    uint32_t k = 0;
+    rc = kv_step_status(&k, clear != 0);
+    if (rc != EVKHIP_OK) return rc;
+    *flags = f | g | k;
     return EVKHIP_OK;
 }
 

@@ -64,6 +64,10 @@ int flash_forward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 int flash_backward(FlashArgs a, int dh, bool mfma, bool causal, hipStream_t st);
 void flash_free_workspace();
 
+// ---- kv_step.hip ----
+int kv_step_status(uint32_t* flags, bool clear);
+void kv_step_free_workspace();
+
 // ---- decode_persist.hip ----
 int decode_status(uint32_t* flags, bool clear);
 void decode_persist_free_workspace();

@@ -712,6 +712,477 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// The d = 256 step on two workgroups per sequence (hidden a multiple of 256
+// up to 1024).  Workgroup j of sequence b takes output columns
+// [128 j, 128 j + 128) of every d-wide product (q, k, v, Wo, W2), hidden
+// columns [j hidden / 2, (j + 1) hidden / 2) of W1, the cached keys k with
+// (k / 16) % 2 == j of the attention and the LM-head blocks of 128 columns
+// j, j + 2, ...; so each streams half of the weights.  After each phase the
+// two swap their halves through 64-bit words in device memory: the payload
+// in the low half, the launch's tag in the high half, written and read at
+// agent scope, so that a word's payload and tag always arrive together.  A
+// mailbox copy is reused two layers later (layer parity), by which time the
+// partner has read it (it cannot start that layer's phase before it has
+// answered the one in between).  Waits are bounded; one that gives up
+// raises a status bit and the step's outputs are then unreliable.  Both
+// workgroups hold identical copies of every full vector (the merges run in
+// workgroup order), so they round the same values the same way.
+// A unit here is 256 rows x 128 columns: a thread owns 8 columns (cg = tid %
+// 16) and 8 rows (kg = tid / 16).
+// ---------------------------------------------------------------------------
+constexpr int UC = 128;         // unit columns
+constexpr int PPART = 8 * UC;   // floats of one unit's wave partials
+constexpr int MBW = 1024;       // mailbox words per (sequence, workgroup, layer parity)
+constexpr int MB_QKV = 0, MB_ATT = 192, MB_X1 = 450, MB_U = 514, MB_X2 = 770;
+static_assert(EVKHIP_KV_MAX_LAYERS * 5 <= 256, "a layer's five tags sit in the tag's low byte");
+
+struct KvPairArgs {
+    KvArgs a;
+    uint64_t* mb;      // (batch, 2, 2, MBW) words
+    uint32_t launch;   // this launch's tag base, >= 1
+    int spin;          // polls before a wait gives up
+};
+
+__device__ unsigned g_kv_pair_status;
+
+DEV void kv_put(uint64_t* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// the payload of *p once it carries `tag` (bounded)
+DEV uint32_t kv_take(const uint64_t* p, uint32_t tag, int spin) {
+    uint64_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int s = 0; (uint32_t)(v >> 32) != tag && s < spin; ++s) {
+        __builtin_amdgcn_s_sleep(1);
+        v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if ((uint32_t)(v >> 32) != tag)
+        __hip_atomic_fetch_or(&g_kv_pair_status, (unsigned)EVKHIP_STATUS_WAIT_TIMEOUT, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    return (uint32_t)v;
+}
+
+int kv_pair_lds_floats(const evkhip_kv_model& m) { return 5 * U + 32 + (int)m.hidden + 4 * PPART + 8; }
+
+__global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
+    extern __shared__ __attribute__((aligned(16))) float kv_smem[];
+    const KvArgs& a = pa.a;
+    const evkhip_kv_model& m = a.m;
+    const int hid = (int)m.hidden, V = (int)m.vocab, NL = (int)m.layers, B = (int)m.batch;
+    const int nh2 = hid / U;             // this workgroup's W1 column units = W2 row units
+    const int b = blockIdx.x % B, j = blockIdx.x / B, pos = a.pos, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int cg = tid & 15, kg = tid >> 4;  // units: 8 of 128 columns, 8 of 256 rows
+    const int c0 = j * UC, pc0 = (j ^ 1) * UC;  // this and the partner's d-wide columns
+    const int h0 = j * (hid / 2), ph0 = (j ^ 1) * (hid / 2);  // and hidden columns
+    float* x = kv_smem;          // U: the residual stream
+    float* q = x + U;            // U
+    float* kk = q + U;           // U
+    float* vv = kk + U;          // U
+    float* o = vv + U;           // U
+    float* ssq = o + U;          // 8: sums of squares of x per wave (waves 0-3)
+    float* smax = ssq + 8;       // 16: the attention's running maximum per wave
+    float* lsum = smax + 16;     // 8: the attention's probability sum per wave
+    float* u = lsum + 8;         // hid: gelu outputs
+    float* part = u + hid;       // 4 x PPART: wave partials
+    float* pstat = part + 4 * PPART;  // 8: the partner's attention maximum and sum
+    uint64_t* mine = pa.mb + (size_t)(b * 2 + j) * 2 * MBW;
+    const uint64_t* theirs = pa.mb + (size_t)(b * 2 + (j ^ 1)) * 2 * MBW;
+    const uint32_t tbase = pa.launch << 8;
+    const int spin = pa.spin;
+
+    const auto Wl = [&](int l, int i) { return static_cast<const f16*>(m.w[l][i]); };
+    const f16* Wout = static_cast<const f16*>(m.w_out);
+    const auto issue = [&](u32x4(&w)[8], const f16* base, uint32_t stride_b, uint32_t bytes, bool ok) {
+        // the operands are uniform; formed in scalar registers so that the
+        // loads need no per-lane descriptor loop
+        const uint64_t bp = reinterpret_cast<uint64_t>(base);
+        base = reinterpret_cast<const f16*>(
+            ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bp >> 32)) << 32) |
+            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)bp));
+        stride_b = (uint32_t)__builtin_amdgcn_readfirstlane((int)stride_b);
+        bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes);
+        const auto r = buf_rsrc(base, bytes);
+        const uint32_t v0 = oob_or(ok, (uint32_t)(kg * 8) * stride_b + (uint32_t)cg * 16);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = buf_load16(r, v0, (uint32_t)i * stride_b);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    constexpr uint32_t UB = U * U * 2;
+    const auto fma8 = [&](const u32x4(&w)[8], const float(&in)[8], float(&acc)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const half8 hw = as_half8(w[i]);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(in[i], (float)hw[c], acc[c]);
+        }
+    };
+    const auto zero8 = [](float(&v)[8]) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = 0.0f;
+    };
+    // the wave's sums of a unit's columns (its four row groups) into part[buf]:
+    // row q of the wave's 16-lane rows stores columns cg * 8 + 2 q, + 1
+    const auto put_part = [&](float(&acc)[8], int buf) {
+        float r[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) r[c] = add_halves(add_row_pairs(acc[c]));
+        const int qr = lane >> 4;
+        const float2 st = qr == 0 ? float2{r[0], r[1]} : qr == 1 ? float2{r[2], r[3]} : qr == 2 ? float2{r[4], r[5]}
+                                                                                      : float2{r[6], r[7]};
+        *reinterpret_cast<float2*>(part + buf * PPART + wave * UC + cg * 8 + 2 * qr) = st;
+    };
+    const auto col_sum = [&](int buf, int n) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) s += part[buf * PPART + w * UC + n];
+        return s;
+    };
+    const auto read8 = [](const float* p, float(&in)[8]) {
+        const float4 v0 = *reinterpret_cast<const float4*>(p);
+        const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
+        in[0] = v0.x, in[1] = v0.y, in[2] = v0.z, in[3] = v0.w;
+        in[4] = v1.x, in[5] = v1.y, in[6] = v1.z, in[7] = v1.w;
+    };
+    // threads 0..U-1 (waves 0-3): ssq[wave] = sum of clamp(x)^2 over the wave
+    const auto sumsq_all = [&]() {
+        if (tid < U) {
+            const float c = fminf(fmaxf(x[tid], -65504.0f), 65504.0f);
+            const float s = add_halves(add_row_pairs(dpp_sum_row16(c * c)));
+            if (lane == 0) ssq[wave] = s;
+        }
+    };
+    float hr[8];  // rms_norm(x) of this thread's rows kg * 8 + i
+    const auto norm_rows = [&]() {
+        const float inv = 1.0f / sqrtf((ssq[0] + ssq[1] + ssq[2] + ssq[3]) / (float)U + m.eps);
+        float xr[8];
+        read8(x + kg * 8, xr);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hr[i] = rnd16(fminf(fmaxf(xr[i], -65504.0f), 65504.0f) * inv);
+    };
+
+    u32x4 wa[8], wb[8];
+    issue(wa, Wl(0, 0) + c0, 2 * U, UB - c0 * 2, true);
+    // rope angles: threads 0..127 take pair c0 / 2 + tid % 64 (q for tid < 64, k after)
+    float rc = 1.0f, rs = 0.0f;
+    if (tid < 128) {
+        const int pr = c0 / 2 + (tid & 63);
+        const float inv_freq = powf(m.rope_base, -2.0f * (float)pr / (float)U);
+        sincosf((float)pos * inv_freq, &rs, &rc);
+    }
+    if (tid < U) {
+        const int tok = min((int)a.ids[b], V - 1);
+        x[tid] = (float)static_cast<const f16*>(m.emb)[(int64_t)tok * U + tid];
+    }
+    __syncthreads();
+    sumsq_all();
+    __syncthreads();
+    const float scale_log2 = 1.4426950408889634f / sqrtf((float)U);
+
+    for (int l = 0; l < NL; ++l) {
+        const uint64_t seq_off = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(b * (int)m.max_seq) * U;
+        f16* Kc = static_cast<f16*>(m.k_cache[l]) + seq_off;
+        f16* Vc = static_cast<f16*>(m.v_cache[l]) + seq_off;
+        uint64_t* mbo = mine + (l & 1) * MBW;
+        const uint64_t* mbi = theirs + (l & 1) * MBW;
+        const uint32_t tg = tbase | (uint32_t)(l * 5);
+        norm_rows();
+        float acc[8];
+        zero8(acc);
+        issue(wb, Wl(l, 1) + c0, 2 * U, UB - c0 * 2, true);
+        fma8(wa, hr, acc);
+        put_part(acc, 0);
+        zero8(acc);
+        issue(wa, Wl(l, 2) + c0, 2 * U, UB - c0 * 2, true);
+        fma8(wb, hr, acc);
+        put_part(acc, 1);
+        zero8(acc);
+        // the attention's first cached keys of this workgroup (kg2 slot: keys
+        // 32 t + 16 j + slot) go out before the v unit is multiplied
+        const int sl = tid >> 5, dg = tid & 31;
+        const auto rK = buf_rsrc(Kc, (uint32_t)pos * U * 2), rV = buf_rsrc(Vc, (uint32_t)pos * U * 2);
+        half8 kp[KB4], vp[KB4];
+#pragma unroll
+        for (int t = 0; t < KB4; ++t) {
+            const int key = 32 * t + 16 * j + sl;
+            kp[t] = as_half8(buf_load16(rK, (uint32_t)(key * U + dg * 8) * 2, 0));
+            vp[t] = as_half8(buf_load16(rV, (uint32_t)(key * U + dg * 8) * 2, 0));
+        }
+        fma8(wa, hr, acc);
+        issue(wb, Wl(l, 3) + c0, 2 * U, UB - c0 * 2, true);
+        put_part(acc, 2);
+        __syncthreads();
+        // this workgroup's q, k (rope) and v columns; the cache row's columns;
+        // the words for the partner
+        if (tid < 192) {
+            const int i = tid & 63, kind = tid >> 6;  // 0 q, 1 k, 2 v: local pair i
+            const float s0 = col_sum(kind, 2 * i), s1 = col_sum(kind, 2 * i + 1);
+            const float a0 = rnd16(s0), a1 = rnd16(s1);
+            float v0, v1;
+            if (kind == 0) {
+                v0 = rnd16(a0 * rc - a1 * rs);
+                v1 = rnd16(a0 * rs + a1 * rc);
+                q[c0 + 2 * i] = v0;
+                q[c0 + 2 * i + 1] = v1;
+            } else if (kind == 1) {
+                v0 = (float)(f16)(a0 * rc - a1 * rs);
+                v1 = (float)(f16)(a0 * rs + a1 * rc);
+                kk[c0 + 2 * i] = v0;
+                kk[c0 + 2 * i + 1] = v1;
+                *reinterpret_cast<uint32_t*>(Kc + (int64_t)pos * U + c0 + 2 * i) = pack_h2(v0, v1);
+            } else {
+                v0 = a0;
+                v1 = a1;
+                vv[c0 + 2 * i] = v0;
+                vv[c0 + 2 * i + 1] = v1;
+                *reinterpret_cast<uint32_t*>(Vc + (int64_t)pos * U + c0 + 2 * i) = pack_h2(v0, v1);
+            }
+            kv_put(mbo + MB_QKV + tid, tg, pack_h2(v0, v1));
+            const uint32_t w = kv_take(mbi + MB_QKV + tid, tg, spin);
+            const float w0 = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xFFFFu));
+            const float w1 = (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
+            float* dst = kind == 0 ? q : kind == 1 ? kk : vv;
+            dst[pc0 + 2 * i] = w0;
+            dst[pc0 + 2 * i + 1] = w1;
+        }
+        __syncthreads();
+
+        // attention over this workgroup's keys: an online softmax per slot
+        float qv[8];
+        read8(q + dg * 8, qv);
+        float m_run = -INFINITY, l_run = 0.0f;
+        zero8(acc);
+        const auto absorb = [&](const half8(&kx)[KB4], const half8(&vx)[KB4], int p0) {
+            float sv[KB4];
+            float mn = m_run;
+#pragma unroll
+            for (int t = 0; t < KB4; ++t) {
+                float d = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kx[t][c], d);
+                sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
+                mn = p0 + 32 * t + 16 * j + sl < pos ? fmaxf(mn, sv[t]) : mn;
+            }
+            const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
+            l_run *= f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] *= f;
+#pragma unroll
+            for (int t = 0; t < KB4; ++t)
+                if (p0 + 32 * t + 16 * j + sl < pos) {
+                    const float pr = exp2f(sv[t] - mn);
+                    l_run += pr;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, (float)vx[t][c], acc[c]);
+                }
+            m_run = mn;
+        };
+        absorb(kp, vp, 0);
+        for (int p0 = 32 * KB4; p0 < pos; p0 += 32 * KB4) {
+#pragma unroll
+            for (int t = 0; t < KB4; ++t) {
+                const int key = p0 + 32 * t + 16 * j + sl;
+                kp[t] = as_half8(buf_load16(rK, (uint32_t)(key * U + dg * 8) * 2, 0));
+                vp[t] = as_half8(buf_load16(rV, (uint32_t)(key * U + dg * 8) * 2, 0));
+            }
+            absorb(kp, vp, p0);
+        }
+        {
+            float kr[8];
+            read8(kk + dg * 8, kr);
+            float d = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], kr[c], d);
+            const float s2 = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
+            if (((pos >> 4) & 1) == j && sl == (pos & 15)) {
+                const float mn = fmaxf(m_run, s2);
+                const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn), pr = exp2f(s2 - mn);
+                float vr[8];
+                read8(vv + dg * 8, vr);
+                l_run = l_run * f + pr;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, vr[c], acc[c] * f);
+                m_run = mn;
+            }
+        }
+        {
+            const auto rm = __builtin_amdgcn_permlane32_swap(__float_as_uint(m_run), __float_as_uint(m_run), false, false);
+            const float m_lo = __uint_as_float(rm[0]), m_hi = __uint_as_float(rm[1]), mw = fmaxf(m_lo, m_hi);
+            const float f_lo = m_lo == -INFINITY ? 0.0f : exp2f(m_lo - mw);
+            const float f_hi = m_hi == -INFINITY ? 0.0f : exp2f(m_hi - mw);
+            float r[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[c]), __float_as_uint(acc[c]), false, false);
+                r[c] = __uint_as_float(t[0]) * f_lo + __uint_as_float(t[1]) * f_hi;
+            }
+            const auto rl = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+            const float lw = __uint_as_float(rl[0]) * f_lo + __uint_as_float(rl[1]) * f_hi;
+            const float4 st = lane < 32 ? float4{r[0], r[1], r[2], r[3]} : float4{r[4], r[5], r[6], r[7]};
+            *reinterpret_cast<float4*>(part + wave * U + dg * 8 + (lane >> 5) * 4) = st;
+            if (lane == 0) {
+                smax[wave] = mw;
+                lsum[wave] = lw;
+            }
+        }
+        __syncthreads();
+        // this workgroup's partial (maximum, sum, numerators) to the partner;
+        // then both partials merged in workgroup order
+        float num = 0.0f, Mj = -INFINITY, den = 0.0f;
+        if (tid < U) {
+#pragma unroll
+            for (int w = 0; w < 8; ++w) Mj = fmaxf(Mj, smax[w]);
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const float f = smax[w] == -INFINITY ? 0.0f : exp2f(smax[w] - Mj);
+                num = __builtin_fmaf(part[w * U + tid], f, num);
+                den = __builtin_fmaf(lsum[w], f, den);
+            }
+            kv_put(mbo + MB_ATT + tid, tg + 1, __float_as_uint(num));
+            if (tid == 0) {
+                kv_put(mbo + MB_ATT + U, tg + 1, __float_as_uint(Mj));
+                kv_put(mbo + MB_ATT + U + 1, tg + 1, __float_as_uint(den));
+            }
+        }
+        float pnum = 0.0f;
+        if (tid < U) pnum = __uint_as_float(kv_take(mbi + MB_ATT + tid, tg + 1, spin));
+        else if (tid < U + 2) pstat[tid - U] = __uint_as_float(kv_take(mbi + MB_ATT + tid, tg + 1, spin));
+        __syncthreads();
+        if (tid < U) {
+            const float pM = pstat[0], pden = pstat[1];
+            const float M0 = j == 0 ? Mj : pM, M1 = j == 0 ? pM : Mj;
+            const float n0 = j == 0 ? num : pnum, n1 = j == 0 ? pnum : num;
+            const float d0v = j == 0 ? den : pden, d1v = j == 0 ? pden : den;
+            const float M = fmaxf(M0, M1);
+            const float f0 = M0 == -INFINITY ? 0.0f : exp2f(M0 - M), f1 = M1 == -INFINITY ? 0.0f : exp2f(M1 - M);
+            const float nt = __builtin_fmaf(n1, f1, n0 * f0), dt = __builtin_fmaf(d1v, f1, d0v * f0);
+            o[tid] = rnd16(nt * (1.0f / dt));
+        }
+        __syncthreads();
+
+        // x = x + fp16(o Wo): this workgroup's columns, then the partner's
+        {
+            float in[8];
+            read8(o + kg * 8, in);
+            zero8(acc);
+            issue(wa, Wl(l, 4) + h0, (uint32_t)hid * 2, (uint32_t)(U * hid - h0) * 2, true);
+            fma8(wb, in, acc);
+            put_part(acc, 1);
+        }
+        __syncthreads();
+        if (tid < UC / 2) {
+            const int i = tid;
+            const float v0 = rnd16(x[c0 + 2 * i] + rnd16(col_sum(1, 2 * i)));
+            const float v1 = rnd16(x[c0 + 2 * i + 1] + rnd16(col_sum(1, 2 * i + 1)));
+            x[c0 + 2 * i] = v0;
+            x[c0 + 2 * i + 1] = v1;
+            kv_put(mbo + MB_X1 + i, tg + 2, pack_h2(v0, v1));
+            const uint32_t w = kv_take(mbi + MB_X1 + i, tg + 2, spin);
+            x[pc0 + 2 * i] = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xFFFFu));
+            x[pc0 + 2 * i + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
+        }
+        __syncthreads();
+        sumsq_all();
+        __syncthreads();
+        norm_rows();
+
+        // MLP units t = 0 .. 2 nh2 - 1: W1 column unit t of this workgroup's
+        // hidden half (t < nh2), then W2 row unit t - nh2 of its output columns
+        float acc2[8];
+        zero8(acc2);
+        const auto next_unit = [&](u32x4(&w)[8], int t) {
+            const bool w1 = t < nh2, w2 = !w1 && t < 2 * nh2, lm = t >= 2 * nh2 && l + 1 == NL;
+            const int vb0 = j * UC;  // the LM head's first block of this workgroup
+            const f16* base = w1   ? Wl(l, 4) + h0 + t * UC
+                              : w2 ? Wl(l, 5) + (int64_t)(t - nh2) * U * U + c0
+                              : lm ? Wout + vb0
+                                   : Wl(l + 1 < NL ? l + 1 : l, 0) + c0;
+            const uint32_t stride_b = w1 ? (uint32_t)hid * 2 : lm ? (uint32_t)V * 2 : 2 * U;
+            const uint32_t bytes = w1   ? (uint32_t)(U * hid - h0 - t * UC) * 2
+                                   : w2 ? (uint32_t)((hid - (t - nh2) * U) * U - c0) * 2
+                                   : lm ? (uint32_t)(U * V - (vb0 < V ? vb0 : 0)) * 2
+                                        : UB - c0 * 2;
+            issue(w, base, stride_b, bytes, !lm || vb0 + cg * 8 < V);
+        };
+        const auto consume_mlp = [&](const u32x4(&w)[8], int t) {
+            if (t < nh2) {
+                float a1[8];
+                zero8(a1);
+                fma8(w, hr, a1);
+                put_part(a1, t);
+                if (t == nh2 - 1) {
+                    __syncthreads();
+                    // this half's gelu outputs, then the partner's
+                    for (int i = tid; i < hid / 4; i += KT) {
+                        const int c = 2 * i;  // local hidden column pair
+                        const float g0 = rnd16(gelu_f(rnd16(col_sum(c / UC, c % UC))));
+                        const float g1 = rnd16(gelu_f(rnd16(col_sum((c + 1) / UC, (c + 1) % UC))));
+                        u[h0 + c] = g0;
+                        u[h0 + c + 1] = g1;
+                        kv_put(mbo + MB_U + i, tg + 3, pack_h2(g0, g1));
+                        const uint32_t wv = kv_take(mbi + MB_U + i, tg + 3, spin);
+                        u[ph0 + c] = (float)__builtin_bit_cast(f16, (uint16_t)(wv & 0xFFFFu));
+                        u[ph0 + c + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(wv >> 16));
+                    }
+                    __syncthreads();
+                }
+            } else {
+                float in[8];
+                read8(u + (t - nh2) * U + kg * 8, in);
+                fma8(w, in, acc2);
+                if (t == 2 * nh2 - 1) {
+                    put_part(acc2, 0);
+                    __syncthreads();
+                    if (tid < UC / 2) {
+                        const int i = tid;
+                        const float v0 = rnd16(x[c0 + 2 * i] + rnd16(col_sum(0, 2 * i)));
+                        const float v1 = rnd16(x[c0 + 2 * i + 1] + rnd16(col_sum(0, 2 * i + 1)));
+                        x[c0 + 2 * i] = v0;
+                        x[c0 + 2 * i + 1] = v1;
+                        kv_put(mbo + MB_X2 + i, tg + 4, pack_h2(v0, v1));
+                        const uint32_t wv = kv_take(mbi + MB_X2 + i, tg + 4, spin);
+                        x[pc0 + 2 * i] = (float)__builtin_bit_cast(f16, (uint16_t)(wv & 0xFFFFu));
+                        x[pc0 + 2 * i + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(wv >> 16));
+                    }
+                    __syncthreads();
+                    sumsq_all();
+                    __syncthreads();
+                }
+            }
+        };
+        for (int t = 0; t < 2 * nh2; t += 2) {
+            next_unit(wb, t + 1);
+            consume_mlp(wa, t);
+            next_unit(wa, t + 2);
+            consume_mlp(wb, t + 1);
+        }
+    }
+
+    // logits: this workgroup's LM-head blocks of 128 columns, j, j + 2, ...
+    norm_rows();
+    f16* lg = a.logits + (int64_t)b * V;
+    const int nvb = (V + UC - 1) / UC;
+    const auto issue_lm = [&](u32x4(&w)[8], int vb) {  // zeros past the last block
+        const int cb = (vb < nvb ? vb : nvb) * UC;
+        issue(w, Wout + cb, (uint32_t)V * 2, (uint32_t)(U * V - cb) * 2, cb + cg * 8 < V);
+    };
+    const auto lm_block = [&](u32x4(&w)[8], int vb, int buf) {
+        float a1[8];
+        zero8(a1);
+        fma8(w, hr, a1);
+        issue_lm(w, vb + 4);
+        put_part(a1, buf);
+        __syncthreads();
+        if (tid < UC && vb * UC + tid < V) lg[vb * UC + tid] = (f16)col_sum(buf, tid);
+    };
+    issue_lm(wb, j + 2);
+    for (int vb = j; vb < nvb; vb += 4) {
+        lm_block(wa, vb, 0);
+        lm_block(wb, vb + 2, 1);
+    }
+}
+
 }  // namespace
 
 int kv_step_lds_bytes(const evkhip_kv_model& m) {
@@ -723,6 +1194,35 @@ int kv_step_lds_bytes(const evkhip_kv_model& m) {
 }  // namespace evkhip
 
 using namespace evkhip;
+
+// ---- the pair step's mailboxes (grow-only; zeroed when allocated) ----
+namespace evkhip {
+namespace {
+struct KvPairWs {
+    uint64_t* mb = nullptr;
+    size_t words = 0;
+    int dev = -1;
+    uint32_t launch = 0;  // tag base of the last launch
+};
+KvPairWs g_kvp;
+}  // namespace
+
+void kv_step_free_workspace() {
+    if (g_kvp.mb) (void)hipFree(g_kvp.mb);
+    g_kvp = KvPairWs{};
+}
+
+int kv_step_status(uint32_t* flags, bool clear) {
+    unsigned v = 0;
+    EVK_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_kv_pair_status), sizeof(v), 0, hipMemcpyDeviceToHost));
+    if (clear && v) {
+        const unsigned zero = 0;
+        EVK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_kv_pair_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice));
+    }
+    *flags = v;
+    return EVKHIP_OK;
+}
+}  // namespace evkhip
 
 extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_t pos, void* logits,
                                      void* stream) {
@@ -763,8 +1263,36 @@ extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* i
     a.ids = ids;
     a.pos = (int)pos;
     a.logits = static_cast<f16*>(logits);
-    hipLaunchKernelGGL(units ? kv_step256 : kv_step, dim3(m->batch), dim3(KT), (unsigned)lds,
-                       reinterpret_cast<hipStream_t>(stream), a);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // two workgroups a sequence where all of them fit on the GPU at once and
+    // the launch is not captured (its tags come from a host counter)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    EVK_HIP(hipStreamIsCapturing(st, &cap));
+    const bool pair = units && cap == hipStreamCaptureStatusNone && 2 * (int64_t)m->batch <= device_cu_count();
+    if (pair) {
+        const size_t words = (size_t)m->batch * 2 * 2 * MBW;
+        if (words > g_kvp.words || g_kvp.dev != dev) {
+            if (g_kvp.mb) EVK_HIP(hipFree(g_kvp.mb));
+            g_kvp = KvPairWs{};
+            EVK_HIP(hipMalloc(&g_kvp.mb, words * sizeof(uint64_t)));
+            EVK_HIP(hipMemsetAsync(g_kvp.mb, 0, words * sizeof(uint64_t), st));
+            g_kvp.words = words;
+            g_kvp.dev = dev;
+        }
+        if (++g_kvp.launch >= (1u << 24)) {  // tags would wrap: start over from clean mailboxes
+            EVK_HIP(hipMemsetAsync(g_kvp.mb, 0, g_kvp.words * sizeof(uint64_t), st));
+            g_kvp.launch = 1;
+        }
+        KvPairArgs pa{};
+        pa.a = a;
+        pa.mb = g_kvp.mb;
+        pa.launch = g_kvp.launch;
+        pa.spin = 1 << 15;  // a hand-over takes a few polls; a wait that gives up marks the status
+        const int plds = kv_pair_lds_floats(*m) * (int)sizeof(float);
+        hipLaunchKernelGGL(kv_step256x2, dim3(2 * m->batch), dim3(KT), (unsigned)plds, st, pa);
+    } else {
+        hipLaunchKernelGGL(units ? kv_step256 : kv_step, dim3(m->batch), dim3(KT), (unsigned)lds, st, a);
+    }
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? EVKHIP_OK : check_hip(e, "kv_decode_step launch");
 }

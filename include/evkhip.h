@@ -360,8 +360,15 @@ int evkhip_model_decode(const evkhip_model_cfg* cfg, const void* weights, void* 
  * EVKHIP_KV_MAX_LAYERS layers and 16-byte aligned pointers, else
  * EVKHIP_ERR_UNSUPPORTED (the op-by-op step serves those shapes).  d = 256
  * with hidden a multiple of 256 up to 1024 (the reference caller's shape)
- * takes a kernel that streams the weights with loads always in flight;
- * other shapes a general one.  The two sum in different orders. */
+ * takes a kernel that streams the weights with loads always in flight,
+ * on two workgroups a sequence that swap their halves of every product in
+ * device memory when all 2 * batch of them fit on the GPU at once and the
+ * stream is not being captured (else on one workgroup a sequence); other
+ * shapes take a general one.  They sum in different orders.  The
+ * two-workgroup waits are bounded: one that gives up raises
+ * EVKHIP_STATUS_WAIT_TIMEOUT (evkhip_device_status) and the outputs of that
+ * call are then unreliable.  Calls that overlap on one GPU race on its
+ * hand-over buffers. */
 #define EVKHIP_KV_MAX_LAYERS 24
 typedef struct evkhip_kv_model {
     uint32_t batch, d, hidden, vocab, layers, max_seq;
