@@ -716,27 +716,35 @@ __global__ __launch_bounds__(KT, 1) void kv_step256(KvArgs a) {
 // ---------------------------------------------------------------------------
 // The d = 256 step on two workgroups per sequence (hidden a multiple of 256
 // up to 1024).  Workgroup j of sequence b takes output columns
-// [128 j, 128 j + 128) of every d-wide product (q, k, v, Wo, W2), hidden
-// columns [j hidden / 2, (j + 1) hidden / 2) of W1, the cached keys k with
-// (k / 16) % 2 == j of the attention and the LM-head blocks of 128 columns
-// j, j + 2, ...; so each streams half of the weights.  After each phase the
-// two swap their halves through 64-bit words in device memory: the payload
-// in the low half, the launch's tag in the high half, written and read at
-// agent scope, so that a word's payload and tag always arrive together.  A
-// mailbox copy is reused two layers later (layer parity), by which time the
-// partner has read it (it cannot start that layer's phase before it has
-// answered the one in between).  Waits are bounded; one that gives up
-// raises a status bit and the step's outputs are then unreliable.  Both
-// workgroups hold identical copies of every full vector (the merges run in
-// workgroup order), so they round the same values the same way.
+// [128 j, 128 j + 128) of q, k and v, the attention's v columns of the same
+// range over every cached key, the rows of Wo that those columns multiply,
+// hidden columns [j hidden / 2, (j + 1) hidden / 2) of W1 and the rows of W2
+// that they multiply, and the LM-head blocks of 128 columns j, j + 2, ...;
+// so each streams half of the weights.  A layer needs three swaps between
+// the two: q and k; the fp32 partial products of Wo (every column); those of
+// W2.  Both add the two partials in the same way, so they hold identical
+// copies of x and round the same values the same way.  The swaps go through
+// 64-bit words in device memory: the payload in the low half, the launch's
+// tag in the high half, written and read at agent scope, so that a word's
+// payload and tag always arrive together.  A mailbox copy is reused two
+// layers later (layer parity), by which time the partner has read it (it
+// cannot start that layer's phase before it has answered the one in
+// between).  Waits are bounded; one that gives up raises a status bit and
+// the step's outputs are then unreliable.
 // A unit here is 256 rows x 128 columns: a thread owns 8 columns (cg = tid %
 // 16) and 8 rows (kg = tid / 16).
 // ---------------------------------------------------------------------------
 constexpr int UC = 128;         // unit columns
 constexpr int PPART = 8 * UC;   // floats of one unit's wave partials
-constexpr int MBW = 1024;       // mailbox words per (sequence, workgroup, layer parity)
-constexpr int MB_QKV = 0, MB_ATT = 192, MB_X1 = 450, MB_U = 514, MB_X2 = 770;
-static_assert(EVKHIP_KV_MAX_LAYERS * 5 <= 256, "a layer's five tags sit in the tag's low byte");
+constexpr int MBW = 640;        // mailbox words per (sequence, workgroup, layer parity)
+constexpr int MB_QK = 0, MB_X1 = 128, MB_X2 = 384;
+static_assert(EVKHIP_KV_MAX_LAYERS * 3 <= 256, "a layer's three tags sit in the tag's low byte");
+constexpr int KBP = 8;          // keys of a slot per attention pass
+
+// four halves at byte offset voff (zeros past the descriptor's end)
+DEV half4 buf_load_h4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+}
 
 struct KvPairArgs {
     KvArgs a;
@@ -775,7 +783,7 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
     const int lane = tid & 63, wave = tid >> 6;
     const int cg = tid & 15, kg = tid >> 4;  // units: 8 of 128 columns, 8 of 256 rows
     const int c0 = j * UC, pc0 = (j ^ 1) * UC;  // this and the partner's d-wide columns
-    const int h0 = j * (hid / 2), ph0 = (j ^ 1) * (hid / 2);  // and hidden columns
+    const int h0 = j * (hid / 2);  // and hidden columns
     float* x = kv_smem;          // U: the residual stream
     float* q = x + U;            // U
     float* kk = q + U;           // U
@@ -784,9 +792,8 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
     float* ssq = o + U;          // 8: sums of squares of x per wave (waves 0-3)
     float* smax = ssq + 8;       // 16: the attention's running maximum per wave
     float* lsum = smax + 16;     // 8: the attention's probability sum per wave
-    float* u = lsum + 8;         // hid: gelu outputs
+    float* u = lsum + 8;         // hid: gelu outputs (this workgroup's half)
     float* part = u + hid;       // 4 x PPART: wave partials
-    float* pstat = part + 4 * PPART;  // 8: the partner's attention maximum and sum
     uint64_t* mine = pa.mb + (size_t)(b * 2 + j) * 2 * MBW;
     const uint64_t* theirs = pa.mb + (size_t)(b * 2 + (j ^ 1)) * 2 * MBW;
     const uint32_t tbase = pa.launch << 8;
@@ -794,7 +801,10 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
 
     const auto Wl = [&](int l, int i) { return static_cast<const f16*>(m.w[l][i]); };
     const f16* Wout = static_cast<const f16*>(m.w_out);
-    const auto issue = [&](u32x4(&w)[8], const f16* base, uint32_t stride_b, uint32_t bytes, bool ok) {
+    // a unit of 256 rows x 128 columns (rows kg * 8 + i, columns cg * 8 ..)
+    // or, rows128, of 128 rows x 256 columns (rows (kg % 16) * 8 + i,
+    // columns (kg / 16) * 128 + cg * 8 ..: waves 0-3 the first 128 columns)
+    const auto issue = [&](u32x4(&w)[8], const f16* base, uint32_t stride_b, uint32_t bytes, bool ok, bool rows128) {
         // the operands are uniform; formed in scalar registers so that the
         // loads need no per-lane descriptor loop
         const uint64_t bp = reinterpret_cast<uint64_t>(base);
@@ -804,7 +814,8 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
         stride_b = (uint32_t)__builtin_amdgcn_readfirstlane((int)stride_b);
         bytes = (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes);
         const auto r = buf_rsrc(base, bytes);
-        const uint32_t v0 = oob_or(ok, (uint32_t)(kg * 8) * stride_b + (uint32_t)cg * 16);
+        const uint32_t v0 = oob_or(ok, rows128 ? (uint32_t)((kg & 15) * 8) * stride_b + (uint32_t)((kg >> 4) * UC + cg * 8) * 2
+                                               : (uint32_t)(kg * 8) * stride_b + (uint32_t)cg * 16);
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = buf_load16(r, v0, (uint32_t)i * stride_b);
         __builtin_amdgcn_sched_barrier(0);
@@ -839,6 +850,11 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
         for (int w = 0; w < 8; ++w) s += part[buf * PPART + w * UC + n];
         return s;
     };
+    // column n (of 256) of a rows128 unit: the partials of waves 4 (n / 128) .. + 3
+    const auto col_sum128 = [&](int buf, int n) {
+        const float* p = part + buf * PPART + (n >> 7) * 4 * UC + (n & 127);
+        return ((p[0] + p[UC]) + p[2 * UC]) + p[3 * UC];
+    };
     const auto read8 = [](const float* p, float(&in)[8]) {
         const float4 v0 = *reinterpret_cast<const float4*>(p);
         const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
@@ -863,7 +879,7 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
     };
 
     u32x4 wa[8], wb[8];
-    issue(wa, Wl(0, 0) + c0, 2 * U, UB - c0 * 2, true);
+    issue(wa, Wl(0, 0) + c0, 2 * U, UB - c0 * 2, true, false);
     // rope angles: threads 0..127 take pair c0 / 2 + tid % 64 (q for tid < 64, k after)
     float rc = 1.0f, rs = 0.0f;
     if (tid < 128) {
@@ -886,105 +902,105 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
         f16* Vc = static_cast<f16*>(m.v_cache[l]) + seq_off;
         uint64_t* mbo = mine + (l & 1) * MBW;
         const uint64_t* mbi = theirs + (l & 1) * MBW;
-        const uint32_t tg = tbase | (uint32_t)(l * 5);
+        const uint32_t tg = tbase | (uint32_t)(l * 3);
         norm_rows();
         float acc[8];
         zero8(acc);
-        issue(wb, Wl(l, 1) + c0, 2 * U, UB - c0 * 2, true);
+        issue(wb, Wl(l, 1) + c0, 2 * U, UB - c0 * 2, true, false);
         fma8(wa, hr, acc);
         put_part(acc, 0);
         zero8(acc);
-        issue(wa, Wl(l, 2) + c0, 2 * U, UB - c0 * 2, true);
+        issue(wa, Wl(l, 2) + c0, 2 * U, UB - c0 * 2, true, false);
         fma8(wb, hr, acc);
         put_part(acc, 1);
         zero8(acc);
-        // the attention's first cached keys of this workgroup (kg2 slot: keys
-        // 32 t + 16 j + slot) go out before the v unit is multiplied
+        // the attention's first cached keys (slot sl: keys 16 t + sl; a lane
+        // scores 8 dimensions and sums 4 of this workgroup's v columns) go
+        // out before the v unit is multiplied; rows past pos read zeros
         const int sl = tid >> 5, dg = tid & 31;
         const auto rK = buf_rsrc(Kc, (uint32_t)pos * U * 2), rV = buf_rsrc(Vc, (uint32_t)pos * U * 2);
-        half8 kp[KB4], vp[KB4];
+        half8 kp[KBP];
+        half4 vp[KBP];
 #pragma unroll
-        for (int t = 0; t < KB4; ++t) {
-            const int key = 32 * t + 16 * j + sl;
+        for (int t = 0; t < KBP; ++t) {
+            const int key = 16 * t + sl;
             kp[t] = as_half8(buf_load16(rK, (uint32_t)(key * U + dg * 8) * 2, 0));
-            vp[t] = as_half8(buf_load16(rV, (uint32_t)(key * U + dg * 8) * 2, 0));
+            vp[t] = buf_load_h4(rV, (uint32_t)(key * U + c0 + dg * 4) * 2);
         }
         fma8(wa, hr, acc);
-        issue(wb, Wl(l, 3) + c0, 2 * U, UB - c0 * 2, true);
+        // Wo rows of this workgroup's o columns, all output columns
+        issue(wb, Wl(l, 3) + (int64_t)c0 * U, 2 * U, (uint32_t)(U - c0) * U * 2, true, true);
         put_part(acc, 2);
         __syncthreads();
         // this workgroup's q, k (rope) and v columns; the cache row's columns;
-        // the words for the partner
+        // q and k swapped with the partner (v stays: each sums its own columns)
         if (tid < 192) {
             const int i = tid & 63, kind = tid >> 6;  // 0 q, 1 k, 2 v: local pair i
             const float s0 = col_sum(kind, 2 * i), s1 = col_sum(kind, 2 * i + 1);
             const float a0 = rnd16(s0), a1 = rnd16(s1);
-            float v0, v1;
             if (kind == 0) {
-                v0 = rnd16(a0 * rc - a1 * rs);
-                v1 = rnd16(a0 * rs + a1 * rc);
+                const float v0 = rnd16(a0 * rc - a1 * rs), v1 = rnd16(a0 * rs + a1 * rc);
                 q[c0 + 2 * i] = v0;
                 q[c0 + 2 * i + 1] = v1;
+                kv_put(mbo + MB_QK + tid, tg, pack_h2(v0, v1));
             } else if (kind == 1) {
-                v0 = (float)(f16)(a0 * rc - a1 * rs);
-                v1 = (float)(f16)(a0 * rs + a1 * rc);
+                const float v0 = (float)(f16)(a0 * rc - a1 * rs), v1 = (float)(f16)(a0 * rs + a1 * rc);
                 kk[c0 + 2 * i] = v0;
                 kk[c0 + 2 * i + 1] = v1;
                 *reinterpret_cast<uint32_t*>(Kc + (int64_t)pos * U + c0 + 2 * i) = pack_h2(v0, v1);
+                kv_put(mbo + MB_QK + tid, tg, pack_h2(v0, v1));
             } else {
-                v0 = a0;
-                v1 = a1;
-                vv[c0 + 2 * i] = v0;
-                vv[c0 + 2 * i + 1] = v1;
-                *reinterpret_cast<uint32_t*>(Vc + (int64_t)pos * U + c0 + 2 * i) = pack_h2(v0, v1);
+                vv[c0 + 2 * i] = a0;
+                vv[c0 + 2 * i + 1] = a1;
+                *reinterpret_cast<uint32_t*>(Vc + (int64_t)pos * U + c0 + 2 * i) = pack_h2(a0, a1);
             }
-            kv_put(mbo + MB_QKV + tid, tg, pack_h2(v0, v1));
-            const uint32_t w = kv_take(mbi + MB_QKV + tid, tg, spin);
-            const float w0 = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xFFFFu));
-            const float w1 = (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
-            float* dst = kind == 0 ? q : kind == 1 ? kk : vv;
-            dst[pc0 + 2 * i] = w0;
-            dst[pc0 + 2 * i + 1] = w1;
+            if (kind < 2) {
+                const uint32_t w = kv_take(mbi + MB_QK + tid, tg, spin);
+                float* dst = kind == 0 ? q : kk;
+                dst[pc0 + 2 * i] = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xFFFFu));
+                dst[pc0 + 2 * i + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
+            }
         }
         __syncthreads();
 
-        // attention over this workgroup's keys: an online softmax per slot
+        // attention over every cached key for this workgroup's v columns: an
+        // online softmax per slot
         float qv[8];
         read8(q + dg * 8, qv);
         float m_run = -INFINITY, l_run = 0.0f;
-        zero8(acc);
-        const auto absorb = [&](const half8(&kx)[KB4], const half8(&vx)[KB4], int p0) {
-            float sv[KB4];
+        float av[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const auto absorb = [&](const half8(&kx)[KBP], const half4(&vx)[KBP], int p0) {
+            float sv[KBP];
             float mn = m_run;
 #pragma unroll
-            for (int t = 0; t < KB4; ++t) {
+            for (int t = 0; t < KBP; ++t) {
                 float d = 0.0f;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kx[t][c], d);
                 sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
-                mn = p0 + 32 * t + 16 * j + sl < pos ? fmaxf(mn, sv[t]) : mn;
+                mn = p0 + 16 * t + sl < pos ? fmaxf(mn, sv[t]) : mn;
             }
             const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
             l_run *= f;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) acc[c] *= f;
+            for (int c = 0; c < 4; ++c) av[c] *= f;
 #pragma unroll
-            for (int t = 0; t < KB4; ++t)
-                if (p0 + 32 * t + 16 * j + sl < pos) {
+            for (int t = 0; t < KBP; ++t)
+                if (p0 + 16 * t + sl < pos) {
                     const float pr = exp2f(sv[t] - mn);
                     l_run += pr;
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, (float)vx[t][c], acc[c]);
+                    for (int c = 0; c < 4; ++c) av[c] = __builtin_fmaf(pr, (float)vx[t][c], av[c]);
                 }
             m_run = mn;
         };
         absorb(kp, vp, 0);
-        for (int p0 = 32 * KB4; p0 < pos; p0 += 32 * KB4) {
+        for (int p0 = 16 * KBP; p0 < pos; p0 += 16 * KBP) {
 #pragma unroll
-            for (int t = 0; t < KB4; ++t) {
-                const int key = p0 + 32 * t + 16 * j + sl;
+            for (int t = 0; t < KBP; ++t) {
+                const int key = p0 + 16 * t + sl;
                 kp[t] = as_half8(buf_load16(rK, (uint32_t)(key * U + dg * 8) * 2, 0));
-                vp[t] = as_half8(buf_load16(rV, (uint32_t)(key * U + dg * 8) * 2, 0));
+                vp[t] = buf_load_h4(rV, (uint32_t)(key * U + c0 + dg * 4) * 2);
             }
             absorb(kp, vp, p0);
         }
@@ -995,14 +1011,15 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], kr[c], d);
             const float s2 = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
-            if (((pos >> 4) & 1) == j && sl == (pos & 15)) {
+            if (sl == (pos & 15)) {
                 const float mn = fmaxf(m_run, s2);
                 const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn), pr = exp2f(s2 - mn);
-                float vr[8];
-                read8(vv + dg * 8, vr);
+                const float4 vr = *reinterpret_cast<const float4*>(vv + c0 + dg * 4);
                 l_run = l_run * f + pr;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) acc[c] = __builtin_fmaf(pr, vr[c], acc[c] * f);
+                av[0] = __builtin_fmaf(pr, vr.x, av[0] * f);
+                av[1] = __builtin_fmaf(pr, vr.y, av[1] * f);
+                av[2] = __builtin_fmaf(pr, vr.z, av[2] * f);
+                av[3] = __builtin_fmaf(pr, vr.w, av[3] * f);
                 m_run = mn;
             }
         }
@@ -1011,99 +1028,76 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
             const float m_lo = __uint_as_float(rm[0]), m_hi = __uint_as_float(rm[1]), mw = fmaxf(m_lo, m_hi);
             const float f_lo = m_lo == -INFINITY ? 0.0f : exp2f(m_lo - mw);
             const float f_hi = m_hi == -INFINITY ? 0.0f : exp2f(m_hi - mw);
-            float r[8];
+            float r[4];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[c]), __float_as_uint(acc[c]), false, false);
+            for (int c = 0; c < 4; ++c) {
+                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(av[c]), __float_as_uint(av[c]), false, false);
                 r[c] = __uint_as_float(t[0]) * f_lo + __uint_as_float(t[1]) * f_hi;
             }
             const auto rl = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
             const float lw = __uint_as_float(rl[0]) * f_lo + __uint_as_float(rl[1]) * f_hi;
-            const float4 st = lane < 32 ? float4{r[0], r[1], r[2], r[3]} : float4{r[4], r[5], r[6], r[7]};
-            *reinterpret_cast<float4*>(part + wave * U + dg * 8 + (lane >> 5) * 4) = st;
+            const float2 st = lane < 32 ? float2{r[0], r[1]} : float2{r[2], r[3]};
+            *reinterpret_cast<float2*>(part + wave * UC + dg * 4 + (lane >> 5) * 2) = st;
             if (lane == 0) {
                 smax[wave] = mw;
                 lsum[wave] = lw;
             }
         }
         __syncthreads();
-        // this workgroup's partial (maximum, sum, numerators) to the partner;
-        // then both partials merged in workgroup order
-        float num = 0.0f, Mj = -INFINITY, den = 0.0f;
-        if (tid < U) {
+        // the waves' partials merged: o over this workgroup's columns
+        if (tid < UC) {
+            float Mw = -INFINITY, num = 0.0f, den = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 8; ++w) Mj = fmaxf(Mj, smax[w]);
+            for (int w = 0; w < 8; ++w) Mw = fmaxf(Mw, smax[w]);
 #pragma unroll
             for (int w = 0; w < 8; ++w) {
-                const float f = smax[w] == -INFINITY ? 0.0f : exp2f(smax[w] - Mj);
-                num = __builtin_fmaf(part[w * U + tid], f, num);
+                const float f = smax[w] == -INFINITY ? 0.0f : exp2f(smax[w] - Mw);
+                num = __builtin_fmaf(part[w * UC + tid], f, num);
                 den = __builtin_fmaf(lsum[w], f, den);
             }
-            kv_put(mbo + MB_ATT + tid, tg + 1, __float_as_uint(num));
-            if (tid == 0) {
-                kv_put(mbo + MB_ATT + U, tg + 1, __float_as_uint(Mj));
-                kv_put(mbo + MB_ATT + U + 1, tg + 1, __float_as_uint(den));
-            }
-        }
-        float pnum = 0.0f;
-        if (tid < U) pnum = __uint_as_float(kv_take(mbi + MB_ATT + tid, tg + 1, spin));
-        else if (tid < U + 2) pstat[tid - U] = __uint_as_float(kv_take(mbi + MB_ATT + tid, tg + 1, spin));
-        __syncthreads();
-        if (tid < U) {
-            const float pM = pstat[0], pden = pstat[1];
-            const float M0 = j == 0 ? Mj : pM, M1 = j == 0 ? pM : Mj;
-            const float n0 = j == 0 ? num : pnum, n1 = j == 0 ? pnum : num;
-            const float d0v = j == 0 ? den : pden, d1v = j == 0 ? pden : den;
-            const float M = fmaxf(M0, M1);
-            const float f0 = M0 == -INFINITY ? 0.0f : exp2f(M0 - M), f1 = M1 == -INFINITY ? 0.0f : exp2f(M1 - M);
-            const float nt = __builtin_fmaf(n1, f1, n0 * f0), dt = __builtin_fmaf(d1v, f1, d0v * f0);
-            o[tid] = rnd16(nt * (1.0f / dt));
+            o[c0 + tid] = rnd16(num * (1.0f / den));
         }
         __syncthreads();
 
-        // x = x + fp16(o Wo): this workgroup's columns, then the partner's
+        // x = x + fp16(o Wo): this workgroup's rows of Wo give a partial of
+        // every column; the partner's partial added (a + b == b + a exactly)
         {
             float in[8];
-            read8(o + kg * 8, in);
+            read8(o + c0 + (kg & 15) * 8, in);
             zero8(acc);
-            issue(wa, Wl(l, 4) + h0, (uint32_t)hid * 2, (uint32_t)(U * hid - h0) * 2, true);
+            issue(wa, Wl(l, 4) + h0, (uint32_t)hid * 2, (uint32_t)(U * hid - h0) * 2, true, false);
             fma8(wb, in, acc);
             put_part(acc, 1);
         }
         __syncthreads();
-        if (tid < UC / 2) {
-            const int i = tid;
-            const float v0 = rnd16(x[c0 + 2 * i] + rnd16(col_sum(1, 2 * i)));
-            const float v1 = rnd16(x[c0 + 2 * i + 1] + rnd16(col_sum(1, 2 * i + 1)));
-            x[c0 + 2 * i] = v0;
-            x[c0 + 2 * i + 1] = v1;
-            kv_put(mbo + MB_X1 + i, tg + 2, pack_h2(v0, v1));
-            const uint32_t w = kv_take(mbi + MB_X1 + i, tg + 2, spin);
-            x[pc0 + 2 * i] = (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xFFFFu));
-            x[pc0 + 2 * i + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
+        if (tid < U) {
+            const float p = col_sum128(1, tid);
+            kv_put(mbo + MB_X1 + tid, tg + 1, __float_as_uint(p));
+            const float pp = __uint_as_float(kv_take(mbi + MB_X1 + tid, tg + 1, spin));
+            x[tid] = rnd16(x[tid] + rnd16(p + pp));
         }
-        __syncthreads();
         sumsq_all();
         __syncthreads();
         norm_rows();
 
         // MLP units t = 0 .. 2 nh2 - 1: W1 column unit t of this workgroup's
-        // hidden half (t < nh2), then W2 row unit t - nh2 of its output columns
+        // hidden half (t < nh2), then W2 rows t - nh2 of that half (128 each)
         float acc2[8];
         zero8(acc2);
         const auto next_unit = [&](u32x4(&w)[8], int t) {
             const bool w1 = t < nh2, w2 = !w1 && t < 2 * nh2, lm = t >= 2 * nh2 && l + 1 == NL;
             const int vb0 = j * UC;  // the LM head's first block of this workgroup
+            const int r2 = h0 + (t - nh2) * UC;  // first W2 row of unit t
             const f16* base = w1   ? Wl(l, 4) + h0 + t * UC
-                              : w2 ? Wl(l, 5) + (int64_t)(t - nh2) * U * U + c0
+                              : w2 ? Wl(l, 5) + (int64_t)r2 * U
                               : lm ? Wout + vb0
                                    : Wl(l + 1 < NL ? l + 1 : l, 0) + c0;
             const uint32_t stride_b = w1 ? (uint32_t)hid * 2 : lm ? (uint32_t)V * 2 : 2 * U;
             const uint32_t bytes = w1   ? (uint32_t)(U * hid - h0 - t * UC) * 2
-                                   : w2 ? (uint32_t)((hid - (t - nh2) * U) * U - c0) * 2
+                                   : w2 ? (uint32_t)(hid - r2) * U * 2
                                    : lm ? (uint32_t)(U * V - (vb0 < V ? vb0 : 0)) * 2
                                         : UB - c0 * 2;
-            issue(w, base, stride_b, bytes, !lm || vb0 + cg * 8 < V);
+            issue(w, base, stride_b, bytes, !lm || vb0 + cg * 8 < V, w2);
         };
         const auto consume_mlp = [&](const u32x4(&w)[8], int t) {
             if (t < nh2) {
@@ -1113,39 +1107,22 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
                 put_part(a1, t);
                 if (t == nh2 - 1) {
                     __syncthreads();
-                    // this half's gelu outputs, then the partner's
-                    for (int i = tid; i < hid / 4; i += KT) {
-                        const int c = 2 * i;  // local hidden column pair
-                        const float g0 = rnd16(gelu_f(rnd16(col_sum(c / UC, c % UC))));
-                        const float g1 = rnd16(gelu_f(rnd16(col_sum((c + 1) / UC, (c + 1) % UC))));
-                        u[h0 + c] = g0;
-                        u[h0 + c + 1] = g1;
-                        kv_put(mbo + MB_U + i, tg + 3, pack_h2(g0, g1));
-                        const uint32_t wv = kv_take(mbi + MB_U + i, tg + 3, spin);
-                        u[ph0 + c] = (float)__builtin_bit_cast(f16, (uint16_t)(wv & 0xFFFFu));
-                        u[ph0 + c + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(wv >> 16));
-                    }
+                    for (int i = tid; i < hid / 2; i += KT) u[h0 + i] = rnd16(gelu_f(rnd16(col_sum(i / UC, i % UC))));
                     __syncthreads();
                 }
             } else {
                 float in[8];
-                read8(u + (t - nh2) * U + kg * 8, in);
+                read8(u + h0 + (t - nh2) * UC + (kg & 15) * 8, in);
                 fma8(w, in, acc2);
                 if (t == 2 * nh2 - 1) {
                     put_part(acc2, 0);
                     __syncthreads();
-                    if (tid < UC / 2) {
-                        const int i = tid;
-                        const float v0 = rnd16(x[c0 + 2 * i] + rnd16(col_sum(0, 2 * i)));
-                        const float v1 = rnd16(x[c0 + 2 * i + 1] + rnd16(col_sum(0, 2 * i + 1)));
-                        x[c0 + 2 * i] = v0;
-                        x[c0 + 2 * i + 1] = v1;
-                        kv_put(mbo + MB_X2 + i, tg + 4, pack_h2(v0, v1));
-                        const uint32_t wv = kv_take(mbi + MB_X2 + i, tg + 4, spin);
-                        x[pc0 + 2 * i] = (float)__builtin_bit_cast(f16, (uint16_t)(wv & 0xFFFFu));
-                        x[pc0 + 2 * i + 1] = (float)__builtin_bit_cast(f16, (uint16_t)(wv >> 16));
+                    if (tid < U) {
+                        const float p = col_sum128(0, tid);
+                        kv_put(mbo + MB_X2 + tid, tg + 2, __float_as_uint(p));
+                        const float pp = __uint_as_float(kv_take(mbi + MB_X2 + tid, tg + 2, spin));
+                        x[tid] = rnd16(x[tid] + rnd16(p + pp));
                     }
-                    __syncthreads();
                     sumsq_all();
                     __syncthreads();
                 }
@@ -1165,7 +1142,7 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
     const int nvb = (V + UC - 1) / UC;
     const auto issue_lm = [&](u32x4(&w)[8], int vb) {  // zeros past the last block
         const int cb = (vb < nvb ? vb : nvb) * UC;
-        issue(w, Wout + cb, (uint32_t)V * 2, (uint32_t)(U * V - cb) * 2, cb + cg * 8 < V);
+        issue(w, Wout + cb, (uint32_t)V * 2, (uint32_t)(U * V - cb) * 2, cb + cg * 8 < V, false);
     };
     const auto lm_block = [&](u32x4(&w)[8], int vb, int buf) {
         float a1[8];
