@@ -65,6 +65,7 @@ SIGNATURES = {
     "evkhip_device_status": (C.c_int, [C.POINTER(C.c_uint32), C.c_int]),
     "evkhip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
     "evkhip_debug_decode_set_epoch": (C.c_int, [C.c_uint32]),
+    "evkhip_debug_kv_set_launch": (C.c_int, [C.c_uint32]),
     "evkhip_flash_has_mfma": (C.c_int, [C.c_uint32]),
     "evkhip_flash_kernel_path": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32]),
     "evkhip_kv_decode_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
@@ -201,6 +202,12 @@ def debug_decode_set_epoch(distance: int) -> None:
     """Test hook: the persistent decode's hand-over tags `distance` below the
     point where they wrap (the next launch needing more clears and restarts)."""
     _check(lib().evkhip_debug_decode_set_epoch(int(distance)))
+
+
+def debug_kv_set_launch(distance: int) -> None:
+    """Test hook: the fused KV decode step's launch counter `distance` launches
+    below the point where its hand-over tags wrap."""
+    _check(lib().evkhip_debug_kv_set_launch(int(distance)))
 
 
 def debug_set_spin_limit(iterations: int) -> None:

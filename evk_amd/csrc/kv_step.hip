@@ -1201,6 +1201,16 @@ int kv_step_status(uint32_t* flags, bool clear) {
 }
 }  // namespace evkhip
 
+extern "C" int evkhip_debug_kv_set_launch(uint32_t distance) {
+    EVK_RETURN_IF(distance == 0 || distance >= (1u << 24), EVKHIP_ERR_INVALID_ARG,
+                  "debug_kv_set_launch: distance %u outside [1, 2^24)", distance);
+    EVK_RETURN_IF(!g_kvp.mb, EVKHIP_ERR_UNSUPPORTED,
+                  "debug_kv_set_launch: no multi-workgroup kv decode step has run in this process");
+    EVK_HIP(hipDeviceSynchronize());
+    g_kvp.launch = (1u << 24) - distance;
+    return EVKHIP_OK;
+}
+
 extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_t pos, void* logits,
                                      void* stream) {
     EVK_RETURN_IF(!m || !ids || !logits || !m->emb || !m->w_out, EVKHIP_ERR_INVALID_ARG,
@@ -1264,7 +1274,8 @@ extern "C" int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* i
         pa.a = a;
         pa.mb = g_kvp.mb;
         pa.launch = g_kvp.launch;
-        pa.spin = 1 << 15;  // a hand-over takes a few polls; a wait that gives up marks the status
+        // a hand-over takes a few polls; a wait that gives up marks the status
+        pa.spin = (int)std::min(flash_spin_limit(), 1u << 15);
         const int plds = kv_pair_lds_floats(*m) * (int)sizeof(float);
         hipLaunchKernelGGL(kv_step256x2, dim3(2 * m->batch), dim3(KT), (unsigned)plds, st, pa);
     } else {

@@ -388,6 +388,13 @@ int evkhip_kv_decode_step(const evkhip_kv_model* m, const uint16_t* ids, uint32_
  * more tags than that clears the mailboxes and restarts them from zero.
  * Synchronises the device; needs a persistent decode to have run on it. */
 int evkhip_debug_decode_set_epoch(uint32_t distance);
+
+/* Test hook of evkhip_kv_decode_step (no reference counterpart): puts the
+ * launch counter that tags the two-workgroup step's hand-overs `distance`
+ * launches below the point where it wraps, so that the launch that reaches
+ * it clears the mailboxes and restarts the tags.  Synchronises the device;
+ * needs a two-workgroup step to have run in this process. */
+int evkhip_debug_kv_set_launch(uint32_t distance);
 uint64_t evkhip_model_packed_elems(const evkhip_model_cfg* cfg);
 int evkhip_model_pack(const evkhip_model_cfg* cfg, const void* weights, void* packed, void* stream);
 int evkhip_model_decode_packed(const evkhip_model_cfg* cfg, const void* packed, void* cache,

@@ -12,6 +12,7 @@
 // rope :1318-1356, rms_norm :1411-1444, greedy :1472-1497, flash backward
 // with Q=K=V=0 :1499-1563.
 #include <evk_ai.h>
+#include <evkhip.h>
 
 #include <cfloat>
 #include <cmath>
@@ -950,8 +951,11 @@ static void test_kv_decoder_matches_full_recompute() {
 // LM-head blocks and positions up to 201 (up to four attention passes of 64
 // keys); d = 128 for the general kernel.  The op-by-op step's ops are each checked against the CPU
 // oracle; the two steps differ only in summation order.
+// wrap > 0: after the first step the fused step's launch counter is put
+// `wrap` launches below the point where its hand-over tags wrap, so later
+// steps cross it (the mailboxes cleared, the tags restarted)
 static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint32_t L, uint32_t V, uint32_t S,
-                                      uint32_t prefix, uint32_t steps) {
+                                      uint32_t prefix, uint32_t steps, uint32_t wrap = 0) {
     std::printf("test_kv_fused_vs_op_by_op(B=%u, D=%u, hidden=%u, layers=%u, vocab=%u, max_seq=%u)\n", B, D, HID, L,
                 V, S);
     srand(1234 + D + HID);
@@ -986,18 +990,23 @@ static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint
     rand_ids(prompt);
     dec.prefill(prompt);
     dec_ops.prefill(prompt);
+    uint32_t flags = 0;
+    TEST(evkhip_device_status(&flags, 1) == EVKHIP_OK);  // start from clear status bits
     float worst = 0.0f, mag = 0.0f;
     for (uint32_t s = 0; s < steps; ++s) {
         rand_ids(ids);
         const std::vector<float> f = download(dec.step(ids));
         const std::vector<float> o = download(dec_ops.step(ids));
+        if (wrap && s == 0) TEST(evkhip_debug_kv_set_launch(wrap) == EVKHIP_OK);
         for (size_t i = 0; i < f.size(); ++i) {
             worst = std::fmax(worst, std::fabs(f[i] - o[i]));
             mag = std::fmax(mag, std::fabs(o[i]));
         }
     }
-    std::printf("  %u steps from position %u: max |fused - op-by-op| %.4g (max |logit| %.4g)\n", steps, prefix,
-                worst, mag);
+    std::printf("  %u steps from position %u%s: max |fused - op-by-op| %.4g (max |logit| %.4g)\n", steps, prefix,
+                wrap ? " across the tag wrap" : "", worst, mag);
+    flags = 1;
+    TEST(evkhip_device_status(&flags, 1) == EVKHIP_OK && flags == 0);
     TEST(dec.cached() == prefix + steps);
     TEST(mag > 0.1f);
     TEST(worst < 1e-2f);
@@ -1088,6 +1097,7 @@ int main(int argc, char** argv) {
     test_graph_tiny_lm();
     test_kv_decoder_matches_full_recompute();
     test_kv_fused_vs_op_by_op(3, 256, 768, 2, 600, 300, 120, 24);
+    test_kv_fused_vs_op_by_op(2, 256, 256, 2, 72, 40, 5, 10, 4);
     // the streamed kernel's edges: one W1/W2 block and a vocabulary under one
     // LM-head block; four W1/W2 blocks, two LM-head blocks and up to four
     // attention passes
