@@ -5,10 +5,11 @@
 // reference samples by recomputing the whole sequence per position
 // (main_llm.cpp:622-654); evk::ai::KVCacheDecoder keeps the keys and values
 // and runs one position per step, op by op (16 launches a layer).  Here one
-// workgroup per sequence runs every layer of the step and the logits in a
-// single launch: at this size (d = 256, 1 MB of weights a layer) a step is
-// bound by launch and memory latency, not by bytes, and a sequence's step
-// needs no exchange with the other sequences.
+// workgroup per sequence (two, at d = 256, where they all fit on the GPU at
+// once) runs every layer of the step and the logits in a single launch: at
+// this size (d = 256, 1 MB of weights a layer) a step is bound by launch and
+// memory latency, not by bytes, and a sequence's step needs no exchange with
+// the other sequences.
 //
 // Rounding follows the op-by-op path (every op output is fp16, sums in
 // fp32), so the step computes what KVCacheDecoder's per-op step computes up
