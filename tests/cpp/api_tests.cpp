@@ -953,9 +953,14 @@ static void test_kv_decoder_matches_full_recompute() {
 // oracle; the two steps differ only in summation order.
 // wrap > 0: after the first step the fused step's launch counter is put
 // `wrap` launches below the point where its hand-over tags wrap, so later
-// steps cross it (the mailboxes cleared, the tags restarted)
+// steps cross it (the mailboxes cleared, the tags restarted).
+// force_timeout: first one fused step of a third decoder with one poll per
+// hand-over wait (evkhip_debug_set_spin_limit(1)): the waits that give up
+// must raise EVKHIP_STATUS_WAIT_TIMEOUT while the kernel still ends; the
+// comparison below then runs with the default limit.
 static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint32_t L, uint32_t V, uint32_t S,
-                                      uint32_t prefix, uint32_t steps, uint32_t wrap = 0) {
+                                      uint32_t prefix, uint32_t steps, uint32_t wrap = 0,
+                                      bool force_timeout = false) {
     std::printf("test_kv_fused_vs_op_by_op(B=%u, D=%u, hidden=%u, layers=%u, vocab=%u, max_seq=%u)\n", B, D, HID, L,
                 V, S);
     srand(1234 + D + HID);
@@ -992,6 +997,16 @@ static void test_kv_fused_vs_op_by_op(uint32_t B, uint32_t D, uint32_t HID, uint
     dec_ops.prefill(prompt);
     uint32_t flags = 0;
     TEST(evkhip_device_status(&flags, 1) == EVKHIP_OK);  // start from clear status bits
+    if (force_timeout) {
+        evk::ai::KVCacheDecoder dec_t(emb, w_out, layers, B, S);
+        dec_t.prefill(prompt);
+        rand_ids(ids);
+        TEST(evkhip_debug_set_spin_limit(1) == EVKHIP_OK);
+        (void)download(dec_t.step(ids));
+        TEST(evkhip_debug_set_spin_limit(0) == EVKHIP_OK);
+        uint32_t forced = 0;
+        TEST(evkhip_device_status(&forced, 1) == EVKHIP_OK && (forced & EVKHIP_STATUS_WAIT_TIMEOUT));
+    }
     float worst = 0.0f, mag = 0.0f;
     for (uint32_t s = 0; s < steps; ++s) {
         rand_ids(ids);
@@ -1102,7 +1117,7 @@ int main(int argc, char** argv) {
     // the streamed kernel's edges: one W1/W2 block and a vocabulary under one
     // LM-head block; four W1/W2 blocks, two LM-head blocks and up to four
     // attention passes
-    test_kv_fused_vs_op_by_op(2, 256, 256, 1, 72, 40, 5, 6);
+    test_kv_fused_vs_op_by_op(2, 256, 256, 1, 72, 40, 5, 6, 0, true);
     test_kv_fused_vs_op_by_op(1, 256, 1024, 1, 264, 240, 190, 12);
     test_kv_fused_vs_op_by_op(2, 128, 256, 2, 200, 64, 9, 8);
     test_timestamps();
