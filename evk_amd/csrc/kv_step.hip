@@ -975,11 +975,16 @@ __global__ __launch_bounds__(KT, 1) void kv_step256x2(KvPairArgs pa) {
             float mn = m_run;
 #pragma unroll
             for (int t = 0; t < KBP; ++t) {
-                float d = 0.0f;
+                sv[t] = 0.0f;
+                // keys 16 t + p0 .. + 15 all at or past pos: no slot scores
+                // (a uniform branch; their loads read zeros and stay)
+                if (p0 + 16 * t < pos) {
+                    float d = 0.0f;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kx[t][c], d);
-                sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
-                mn = p0 + 16 * t + sl < pos ? fmaxf(mn, sv[t]) : mn;
+                    for (int c = 0; c < 8; ++c) d = __builtin_fmaf(qv[c], (float)kx[t][c], d);
+                    sv[t] = add_row_pairs(dpp_sum_row16(d)) * scale_log2;
+                    mn = p0 + 16 * t + sl < pos ? fmaxf(mn, sv[t]) : mn;
+                }
             }
             const float f = m_run == -INFINITY ? 0.0f : exp2f(m_run - mn);
             l_run *= f;
