@@ -1114,6 +1114,7 @@ int main(int argc, char** argv) {
     test_kv_fused_vs_op_by_op(3, 256, 768, 2, 600, 300, 120, 24);
     test_kv_fused_vs_op_by_op(2, 256, 256, 2, 72, 40, 5, 10, 4);
     test_kv_fused_vs_op_by_op(128, 256, 256, 1, 72, 40, 5, 3);  // 2 x 128 workgroups: every CU of an MI355X
+    test_kv_fused_vs_op_by_op(129, 256, 256, 1, 72, 40, 5, 3);  // 2 x 129 > 256 CUs: one workgroup a sequence
     // the streamed kernel's edges: one W1/W2 block and a vocabulary under one
     // LM-head block; four W1/W2 blocks, two LM-head blocks and up to four
     // attention passes
